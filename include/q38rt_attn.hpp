@@ -1,0 +1,140 @@
+// q38rt_attn.hpp -- header-only C++ shim that re-creates the reference runtime's attention / KV-cache operator
+// signatures (namespace q38rt::cuda, src/cuda/ops.cuh:99-140 and src/cuda/prefill.cuh:46-62) on top of the C ABI in
+// qwattn.h, so the engine's call sites (src/runtime/engine.cpp:1587-1592, 2457-2479) compile unchanged against the
+// MI355X library.  The stream type is hipStream_t; fp16 outputs are uint16_t bits (the reference's __half).
+// Like the reference, a rejected call prints the reason and aborts (src/cuda/ops.cu:1002-1008).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+
+#include "qwattn.h"
+
+namespace q38rt {
+namespace cuda {
+
+enum class KVType : int { F16 = QWA_KV_F16, Q8_0 = QWA_KV_Q8_0, Q4_0 = QWA_KV_Q4_0 };
+
+struct KVLayer {
+    uint8_t* k = nullptr;
+    uint8_t* v = nullptr;
+    uint16_t* ks = nullptr;
+    uint16_t* vs = nullptr;
+    int capacity = 0;
+};
+
+struct ActQ8 {
+    int8_t* q = nullptr;
+    float* d = nullptr;
+    float* s = nullptr;
+};
+
+struct RowSrc {
+    const float* dev = nullptr;
+    const float* host = nullptr;
+    int split = 0, host_ld = 0;
+    static RowSrc device(const float* p, int n) {
+        RowSrc s;
+        s.dev = p;
+        s.split = n;
+        return s;
+    }
+    static RowSrc split_at(const float* dev, int split, const float* host, int host_ld) {
+        RowSrc s;
+        s.dev = dev;
+        s.split = split;
+        s.host = host;
+        s.host_ld = host_ld;
+        return s;
+    }
+};
+
+namespace detail {
+inline void check(int status, const char* fn) {
+    if (status != QWA_OK) {
+        std::fprintf(stderr, "%s: %s (%s)\n", fn, qwa_status_string(status), qwa_last_error());
+        std::abort();
+    }
+}
+inline qwa_kv_layer c(const KVLayer& kv) { return qwa_kv_layer{kv.k, kv.v, kv.ks, kv.vs, kv.capacity}; }
+inline qwa_row_src c(const RowSrc& s) { return qwa_row_src{s.dev, s.host, s.split, s.host_ld}; }
+}  // namespace detail
+
+inline size_t kv_value_bytes(KVType t) { return qwa_kv_value_bytes((int)t); }
+inline size_t kv_scale_bytes(KVType t) { return qwa_kv_scale_bytes((int)t); }
+
+inline void attn_prep(const float* qg, const float* k, const float* v, const float* q_norm, const float* k_norm, int pos,
+                      float theta, float eps, KVType kvt, KVLayer& kv, float* q_out, float* gate, hipStream_t st) {
+    const qwa_kv_layer l = detail::c(kv);
+    detail::check(qwa_attn_prep(qg, k, v, q_norm, k_norm, pos, theta, eps, (int)kvt, &l, q_out, gate, st), "attn_prep");
+}
+
+inline void attn_prep_multi(const RowSrc& qg, const RowSrc& k, const RowSrc& v, const float* q_norm,
+                            const float* k_norm, int pos0, int rope_pos0, int n, float theta, float eps, KVType kvt,
+                            KVLayer& kv, float* q_out, float* gate, hipStream_t st) {
+    const qwa_kv_layer l = detail::c(kv);
+    const qwa_row_src a = detail::c(qg), b = detail::c(k), c = detail::c(v);
+    detail::check(qwa_attn_prep_multi(&a, &b, &c, q_norm, k_norm, pos0, rope_pos0, n, theta, eps, (int)kvt, &l, q_out,
+                                      gate, st),
+                  "attn_prep_multi");
+}
+
+inline size_t attn_work_bytes(int n_pos) { return qwa_attn_work_bytes(n_pos); }
+inline int attn_max_positions() { return qwa_attn_max_positions(); }
+
+inline void attn_decode(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int n_pos, void* work,
+                        float* out, const ActQ8* oq, hipStream_t st) {
+    const qwa_kv_layer l = detail::c(kv);
+    const qwa_act_q8 a = oq ? qwa_act_q8{oq->q, oq->d, oq->s} : qwa_act_q8{nullptr, nullptr, nullptr};
+    detail::check(qwa_attn_decode(q, gate, &l, (int)kvt, n_pos, work, out, oq ? &a : nullptr, st), "attn_decode");
+}
+
+inline void attn_decode_multi(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int pos0, int nq,
+                              void* work, float* out, const ActQ8* oq, hipStream_t st, float* out_host = nullptr) {
+    const qwa_kv_layer l = detail::c(kv);
+    const qwa_act_q8 a = oq ? qwa_act_q8{oq->q, oq->d, oq->s} : qwa_act_q8{nullptr, nullptr, nullptr};
+    detail::check(qwa_attn_decode_multi(q, gate, &l, (int)kvt, pos0, nq, work, out, oq ? &a : nullptr, st, out_host),
+                  "attn_decode_multi");
+}
+
+inline void attn_decode_simple(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int n_pos, void* work,
+                               float* out, const ActQ8* oq, hipStream_t st) {
+    const qwa_kv_layer l = detail::c(kv);
+    const qwa_act_q8 a = oq ? qwa_act_q8{oq->q, oq->d, oq->s} : qwa_act_q8{nullptr, nullptr, nullptr};
+    detail::check(qwa_attn_decode_simple(q, gate, &l, (int)kvt, n_pos, work, out, oq ? &a : nullptr, st),
+                  "attn_decode_simple");
+}
+
+inline void rope_table(int p0, int B, float theta, float* rope, hipStream_t st) {
+    detail::check(qwa_rope_table(p0, B, theta, rope, st), "rope_table");
+}
+
+inline void rope_table_pos(const int* pos, int B, float theta, float* rope, hipStream_t st) {
+    detail::check(qwa_rope_table_pos(pos, B, theta, rope, st), "rope_table_pos");
+}
+
+inline void attn_prep_rows(const float* qg, const float* k, const float* v, const float* q_norm, const float* k_norm,
+                           int B, int p0, const float* rope, float eps, KVType kvt, KVLayer& kv, float* q, float* gate,
+                           hipStream_t st) {
+    const qwa_kv_layer l = detail::c(kv);
+    detail::check(qwa_attn_prep_rows(qg, k, v, q_norm, k_norm, B, p0, rope, eps, (int)kvt, &l, q, gate, st),
+                  "attn_prep_rows");
+}
+
+inline void attn_prefill(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int B, int p0,
+                         uint16_t* out16, hipStream_t st) {
+    const qwa_kv_layer l = detail::c(kv);
+    detail::check(qwa_attn_prefill(q, gate, &l, (int)kvt, B, p0, out16, st), "attn_prefill");
+}
+
+inline void attn_prefill_simple(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int B, int p0,
+                                uint16_t* out16, hipStream_t st) {
+    const qwa_kv_layer l = detail::c(kv);
+    detail::check(qwa_attn_prefill_simple(q, gate, &l, (int)kvt, B, p0, out16, st), "attn_prefill_simple");
+}
+
+}  // namespace cuda
+}  // namespace q38rt

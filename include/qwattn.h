@@ -1,0 +1,131 @@
+/*
+ * qwattn.h -- C ABI of the MI355X (gfx950) gated-attention path.
+ *
+ * Drop-in replacement for the attention / KV-cache operators of the reference runtime (namespace q38rt::cuda,
+ * src/cuda/ops.cuh and src/cuda/prefill.cuh).  Every entry point below names the reference declaration it
+ * replaces.  Conventions:
+ *   - all tensors are caller-owned device memory (out_host: host memory mapped for device access);
+ *   - `stream` is a hipStream_t (NULL = the default stream); every call is asynchronous and stream-ordered;
+ *   - no entry point allocates memory; the decode `work` buffer is sized by qwa_attn_work_bytes();
+ *   - the return value is a status code (QWA_OK = 0).  Invalid arguments are rejected before anything is launched
+ *     (the reference aborts in the same situations, src/cuda/ops.cu:1002-1008); the C++ shim in q38rt_attn.hpp
+ *     turns a nonzero status into abort() exactly like the reference.
+ * Shapes are fixed by the model: 24 query heads, 4 KV heads (GQA group 6), head_dim 256, 64 rotary dims.
+ */
+#ifndef QWATTN_H
+#define QWATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum {
+    QWA_OK = 0,
+    QWA_ERR_INVALID = 1,   /* bad argument (null pointer, unknown KV type, nq out of range, ...) */
+    QWA_ERR_RANGE = 2,     /* context or position beyond what the kernels / the cache capacity support */
+    QWA_ERR_HIP = 3,       /* a HIP runtime call (launch) failed */
+};
+
+/* KV cache element type.  Replaces q38rt::cuda::KVType (src/cuda/ops.cuh:99). */
+enum { QWA_KV_F16 = 0, QWA_KV_Q8_0 = 1, QWA_KV_Q4_0 = 2 };
+
+/* Per-layer KV cache, split layout.  Replaces q38rt::cuda::KVLayer (src/cuda/ops.cuh:106-113).
+ * values k, v: [4 kv heads][capacity positions][qwa_kv_value_bytes] (16-byte aligned rows);
+ * scales ks, vs: [4][capacity][8] fp16 bits (Q8_0 / Q4_0 only; may be NULL for F16). */
+typedef struct {
+    uint8_t* k;
+    uint8_t* v;
+    uint16_t* ks;
+    uint16_t* vs;
+    int capacity;
+} qwa_kv_layer;
+
+/* int8 activations with per-32 scale d and s = d * sum(q).  Replaces q38rt::cuda::ActQ8 (src/cuda/gemv.cuh:14-18). */
+typedef struct {
+    int8_t* q;
+    float* d;
+    float* s;
+} qwa_act_q8;
+
+/* Row source: element i of row r is dev[r*n + i] for i < split, else host[r*host_ld + i - split] (mapped host
+ * memory).  Replaces q38rt::cuda::RowSrc (src/cuda/ops.cuh:24-34). */
+typedef struct {
+    const float* dev;
+    const float* host;
+    int split;
+    int host_ld;
+} qwa_row_src;
+
+/* Bytes of one 256-value head row / of its scales.  Replace kv_value_bytes / kv_scale_bytes
+ * (src/cuda/ops.cuh:103-104, src/cuda/ops.cu:966-974).  0 for an unknown type. */
+size_t qwa_kv_value_bytes(int kvt);
+size_t qwa_kv_scale_bytes(int kvt);
+
+/* Replaces attn_prep (src/cuda/ops.cuh:117-118): q/k per-head RMSNorm, NeoX RoPE on dims [0,64), gate split,
+ * K/V quantize-on-append at cache position `pos`.  qg [24][512] (q | gate per head), k, v [4][256]. */
+int qwa_attn_prep(const float* qg, const float* k, const float* v, const float* q_norm, const float* k_norm, int pos,
+                  float theta, float eps, int kvt, const qwa_kv_layer* kv, float* q_out, float* gate, void* stream);
+
+/* Replaces attn_prep_multi (src/cuda/ops.cuh:122-124): n tokens at cache positions pos0.. and rotary positions
+ * rope_pos0..; qg / k / v rows of 12288 / 1024 / 1024 floats from split device / mapped-host sources. */
+int qwa_attn_prep_multi(const qwa_row_src* qg, const qwa_row_src* k, const qwa_row_src* v, const float* q_norm,
+                        const float* k_norm, int pos0, int rope_pos0, int n, float theta, float eps, int kvt,
+                        const qwa_kv_layer* kv, float* q_out, float* gate, void* stream);
+
+/* Replaces attn_work_bytes (src/cuda/ops.cuh:129): size of the decode scratch for contexts up to n_pos positions
+ * (covers up to 8 queries per call and the FP32 test kernel). */
+size_t qwa_attn_work_bytes(int n_pos);
+/* Replaces attn_max_positions (src/cuda/ops.cuh:131): 262144. */
+int qwa_attn_max_positions(void);
+
+/* Replaces attn_decode (src/cuda/ops.cuh:132-133): one query over positions [0, n_pos). */
+int qwa_attn_decode(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int n_pos, void* work,
+                    float* out, const qwa_act_q8* oq, void* stream);
+
+/* Replaces attn_decode_multi (src/cuda/ops.cuh:136-137): nq (1..8) queries at positions pos0..pos0+nq-1, query t
+ * seeing keys [0, pos0+t].  q / gate / out rows of 6144 floats; optional ActQ8 rows and a copy of out in mapped host
+ * memory.  Each query's result is bit-identical to qwa_attn_decode on it alone. */
+int qwa_attn_decode_multi(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int pos0, int nq,
+                          void* work, float* out, const qwa_act_q8* oq, void* stream, float* out_host);
+
+/* Replaces attn_decode_simple (src/cuda/ops.cuh:139-140): FP32 vector-ALU kernel kept for tests. */
+int qwa_attn_decode_simple(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int n_pos, void* work,
+                           float* out, const qwa_act_q8* oq, void* stream);
+
+/* Replace rope_table / rope_table_pos (src/cuda/prefill.cuh:46-52): rope [B][64] = cos[32] | sin[32] of
+ * pos * theta^(-2i/64); pos = p0 + t, or (M-RoPE) pos3[t*3 + i%3] from a device array [B][3]. */
+int qwa_rope_table(int p0, int B, float theta, float* rope, void* stream);
+int qwa_rope_table_pos(const int* pos3, int B, float theta, float* rope, void* stream);
+
+/* Replaces attn_prep_rows (src/cuda/prefill.cuh:55-56): prep of B prefill tokens at cache positions p0.. using a
+ * rope table; qg [B][12288], k / v [B][1024]; writes q / gate [B][6144] and appends K/V. */
+int qwa_attn_prep_rows(const float* qg, const float* k, const float* v, const float* q_norm, const float* k_norm,
+                       int B, int p0, const float* rope, float eps, int kvt, const qwa_kv_layer* kv, float* q,
+                       float* gate, void* stream);
+
+/* Replaces attn_prefill (src/cuda/prefill.cuh:59-60): causal attention of B queries at positions p0..p0+B-1 over
+ * the cache [0, p0+B), output * sigmoid(gate) as fp16 bits [B][6144].  fp16 MFMA, fp32 accumulation. */
+int qwa_attn_prefill(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
+                     uint16_t* out16, void* stream);
+
+/* Replaces attn_prefill_simple (src/cuda/prefill.cuh:61-62): FP32 vector-ALU version kept for tests. */
+int qwa_attn_prefill_simple(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
+                            uint16_t* out16, void* stream);
+
+/* Quantize-on-append of raw rows, without the norm / RoPE of prep: rows x [n][4][256] stored at positions pos0..
+ * of every KV head, for K (xk) and V (xv); either may be NULL.  The store is the reference's kv_store_row
+ * (src/cuda/common.cuh:199-228), exposed on its own so callers holding already-roped K can append them. */
+int qwa_kv_append(const float* xk, const float* xv, int pos0, int n, int kvt, const qwa_kv_layer* kv, void* stream);
+
+/* Human-readable text of a status code, and of the last error recorded by this library in the calling thread. */
+const char* qwa_status_string(int status);
+const char* qwa_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

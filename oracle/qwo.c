@@ -1,0 +1,409 @@
+/*
+ * qwo.c -- CPU oracle for the gated-attention hot path.  TEST INFRASTRUCTURE ONLY: loaded by tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker / CPU baseline, never by the product.
+ *
+ * Compiled with -ffp-contract=off (no FMA contraction) so the quantizers round exactly like the reference's
+ * scalar code (the reference builds src/quant/quant_ref.cpp with the same flag, CMakeLists.txt:66-68).
+ */
+#include "qwo.h"
+
+#include <math.h>
+#include <omp.h>
+#include <stdlib.h>
+#include <string.h>
+
+#if defined(__AVX2__) && defined(__FMA__)
+#include <immintrin.h>
+#define QWO_HAVE_AVX2 1
+#endif
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * fp16 <-> fp32, exact IEEE binary16 with round-to-nearest-even.  Semantics of src/quant/quant_formats.h:29-78.
+ * ------------------------------------------------------------------------------------------------------------- */
+float qwo_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const int e = (h >> 10) & 31;
+    const uint32_t m = h & 1023u;
+    uint32_t bits;
+    if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13); /* inf / nan keep their payload */
+    } else if (e == 0) {
+        /* zero or subnormal: value is m * 2^-24, exactly representable in fp32 */
+        float f = (float)m * 5.9604644775390625e-08f;
+        memcpy(&bits, &f, 4);
+        bits |= sign;
+    } else {
+        bits = sign | ((uint32_t)(e - 15 + 127) << 23) | (m << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+uint16_t qwo_fp32_to_fp16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u); /* nan -> quiet nan */
+    if (ax == 0x7F800000u) return (uint16_t)(sign | 0x7C00u);
+    const int e = (int)(ax >> 23) - 127; /* unbiased exponent of the fp32 value */
+    if (e >= 16) return (uint16_t)(sign | 0x7C00u);
+    uint32_t mant = (ax & 0x7FFFFFu) | (ax >= 0x00800000u ? 0x800000u : 0u);
+    int shift; /* number of low mantissa bits dropped */
+    uint32_t base;
+    if (e >= -14) {
+        /* normal fp16: keep 10 fraction bits */
+        shift = 13;
+        base = ((uint32_t)(e + 15) << 10);
+        mant &= 0x7FFFFFu;
+    } else {
+        /* subnormal fp16: value = mant * 2^(e-23) expressed in units of 2^-24 */
+        shift = 13 + (-14 - e);
+        if (ax < 0x00800000u) return sign; /* fp32 subnormals are far below fp16's range */
+        if (shift > 24) return sign;
+        base = 0;
+    }
+    uint32_t q = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    /* a carry out of the fraction correctly bumps the exponent (or turns the max normal into inf) */
+    return (uint16_t)(sign | (base + q));
+}
+
+void qwo_fp32_to_fp16_n(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = qwo_fp32_to_fp16(x[i]);
+}
+void qwo_fp16_to_fp32_n(const uint16_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = qwo_fp16_to_fp32(x[i]);
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * ggml Q8_0 / Q4_0 block quantizers: src/quant/quant_ref.cpp:507-538.
+ * ------------------------------------------------------------------------------------------------------------- */
+void qwo_quantize_q8_0(const float* x, uint8_t* blocks, int64_t n) {
+    for (int64_t b = 0; b < n / 32; b++) {
+        const float* xb = x + 32 * b;
+        uint8_t* out = blocks + 34 * b;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) {
+            const float a = fabsf(xb[j]);
+            if (a > amax) amax = a;
+        }
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t dh = qwo_fp32_to_fp16(d);
+        memcpy(out, &dh, 2);
+        for (int j = 0; j < 32; j++) {
+            const float r = roundf(xb[j] * id); /* half away from zero */
+            out[2 + j] = (uint8_t)(int8_t)(int)r;
+        }
+    }
+}
+
+void qwo_quantize_q4_0(const float* x, uint8_t* blocks, int64_t n) {
+    for (int64_t b = 0; b < n / 32; b++) {
+        const float* xb = x + 32 * b;
+        uint8_t* out = blocks + 18 * b;
+        /* max = signed value of the FIRST element of largest magnitude */
+        float amax = 0.0f, mx = 0.0f;
+        for (int j = 0; j < 32; j++) {
+            const float a = fabsf(xb[j]);
+            if (a > amax) {
+                amax = a;
+                mx = xb[j];
+            }
+        }
+        const float d = mx / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t dh = qwo_fp32_to_fp16(d);
+        memcpy(out, &dh, 2);
+        for (int j = 0; j < 16; j++) {
+            const float t0 = xb[j] * id;
+            const float t1 = xb[j + 16] * id;
+            /* truncating conversion through int8, then clamp to 15 */
+            int c0 = (int)(int8_t)(int)(t0 + 8.5f);
+            int c1 = (int)(int8_t)(int)(t1 + 8.5f);
+            if (c0 > 15) c0 = 15;
+            if (c1 > 15) c1 = 15;
+            out[2 + j] = (uint8_t)((c0 & 15) | ((c1 & 15) << 4));
+        }
+    }
+}
+
+void qwo_dequantize_q8_0(const uint8_t* blocks, float* y, int64_t n) {
+    for (int64_t b = 0; b < n / 32; b++) {
+        uint16_t dh;
+        memcpy(&dh, blocks + 34 * b, 2);
+        const float d = qwo_fp16_to_fp32(dh);
+        for (int j = 0; j < 32; j++) y[32 * b + j] = (float)(int8_t)blocks[34 * b + 2 + j] * d;
+    }
+}
+
+void qwo_dequantize_q4_0(const uint8_t* blocks, float* y, int64_t n) {
+    for (int64_t b = 0; b < n / 32; b++) {
+        uint16_t dh;
+        memcpy(&dh, blocks + 18 * b, 2);
+        const float d = qwo_fp16_to_fp32(dh);
+        for (int j = 0; j < 16; j++) {
+            const uint8_t byte = blocks[18 * b + 2 + j];
+            y[32 * b + j] = (float)((int)(byte & 15) - 8) * d;
+            y[32 * b + j + 16] = (float)((int)(byte >> 4) - 8) * d;
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Split KV layout (src/cuda/ops.cuh:99-113, src/cuda/common.cuh:199-228): the same quantizer values as ggml's
+ * blocks, regrouped per 256-value row into contiguous values + 8 fp16 scales, Q4_0 codes pairwise (2i low, 2i+1 high).
+ * ------------------------------------------------------------------------------------------------------------- */
+size_t qwo_kv_value_bytes(int kvt) {
+    return kvt == QWO_F16 ? 512u : kvt == QWO_Q8_0 ? 256u : kvt == QWO_Q4_0 ? 128u : 0u;
+}
+size_t qwo_kv_scale_bytes(int kvt) { return kvt == QWO_Q8_0 || kvt == QWO_Q4_0 ? 16u : 0u; }
+
+void qwo_kv_store_rows(int kvt, const float* x, int64_t nrows, uint8_t* vals, uint16_t* scales) {
+    const size_t vb = qwo_kv_value_bytes(kvt);
+    for (int64_t r = 0; r < nrows; r++) {
+        const float* xr = x + 256 * r;
+        uint8_t* vr = vals + vb * r;
+        if (kvt == QWO_F16) {
+            for (int i = 0; i < 256; i++) {
+                const uint16_t h = qwo_fp32_to_fp16(xr[i]);
+                memcpy(vr + 2 * i, &h, 2);
+            }
+            continue;
+        }
+        uint16_t* sr = scales + 8 * r;
+        for (int b = 0; b < 8; b++) {
+            uint8_t blk[34];
+            if (kvt == QWO_Q8_0) {
+                qwo_quantize_q8_0(xr + 32 * b, blk, 32);
+                memcpy(&sr[b], blk, 2);
+                memcpy(vr + 32 * b, blk + 2, 32);
+            } else {
+                qwo_quantize_q4_0(xr + 32 * b, blk, 32);
+                memcpy(&sr[b], blk, 2);
+                uint8_t codes[32];
+                for (int j = 0; j < 16; j++) {
+                    codes[j] = blk[2 + j] & 15;
+                    codes[j + 16] = blk[2 + j] >> 4;
+                }
+                for (int i = 0; i < 16; i++) vr[16 * b + i] = (uint8_t)(codes[2 * i] | (codes[2 * i + 1] << 4));
+            }
+        }
+    }
+}
+
+void qwo_kv_load_rows(int kvt, const uint8_t* vals, const uint16_t* scales, int64_t nrows, float* out) {
+    const size_t vb = qwo_kv_value_bytes(kvt);
+    for (int64_t r = 0; r < nrows; r++) {
+        const uint8_t* vr = vals + vb * r;
+        float* o = out + 256 * r;
+        if (kvt == QWO_F16) {
+            for (int i = 0; i < 256; i++) {
+                uint16_t h;
+                memcpy(&h, vr + 2 * i, 2);
+                o[i] = qwo_fp16_to_fp32(h);
+            }
+            continue;
+        }
+        const uint16_t* sr = scales + 8 * r;
+        for (int i = 0; i < 256; i++) {
+            const float d = qwo_fp16_to_fp32(sr[i / 32]);
+            int c;
+            if (kvt == QWO_Q8_0) c = (int8_t)vr[i];
+            else c = (int)((vr[i / 2] >> (4 * (i & 1))) & 15) - 8;
+            o[i] = (float)c * d;
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Gated attention: src/reference/ref_model.cpp:195-219 (+ :104 sigmoid).  Scores in double, softmax in double,
+ * P.V accumulated in double, normalised, then multiplied by sigmoid(gate).
+ * ------------------------------------------------------------------------------------------------------------- */
+
+/* The reference CPU dot product (src/reference/ref_model.cpp:79-95): four 8-lane fp32 FMA accumulators over
+ * 32-element steps, lanes summed pairwise in fp32, the 8 lanes then summed in double. */
+static float dot_ref(const float* a, const float* b, int n) {
+#ifdef QWO_HAVE_AVX2
+    __m256 acc[4] = {_mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps()};
+    int i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int u = 0; u < 4; u++)
+            acc[u] = _mm256_fmadd_ps(_mm256_loadu_ps(a + i + 8 * u), _mm256_loadu_ps(b + i + 8 * u), acc[u]);
+    const __m256 s = _mm256_add_ps(_mm256_add_ps(acc[0], acc[1]), _mm256_add_ps(acc[2], acc[3]));
+    float lanes[8];
+    _mm256_storeu_ps(lanes, s);
+    double total = 0.0;
+    for (int j = 0; j < 8; j++) total += lanes[j];
+    for (; i < n; i++) total += (double)a[i] * b[i];
+    return (float)total;
+#else
+    float lanes[4][8];
+    memset(lanes, 0, sizeof lanes);
+    int i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int u = 0; u < 4; u++)
+            for (int j = 0; j < 8; j++) lanes[u][j] = fmaf(a[i + 8 * u + j], b[i + 8 * u + j], lanes[u][j]);
+    double total = 0.0;
+    for (int j = 0; j < 8; j++) total += (double)((lanes[0][j] + lanes[1][j]) + (lanes[2][j] + lanes[3][j]));
+    for (; i < n; i++) total += (double)a[i] * b[i];
+    return (float)total;
+#endif
+}
+
+static double dot_exact(const float* a, const float* b, int n) {
+    double s = 0.0;
+    for (int i = 0; i < n; i++) s += (double)a[i] * (double)b[i];
+    return s;
+}
+
+void qwo_attention(const float* q, const float* gate, const float* K, const float* V, int64_t ld, int pos0, int nq,
+                   int mode, int threads, float* out) {
+    const int nthr = threads > 0 ? threads : omp_get_max_threads();
+#pragma omp parallel num_threads(nthr)
+    {
+        const int64_t maxpos = (int64_t)pos0 + nq;
+        double* s = (double*)malloc(sizeof(double) * (size_t)maxpos);
+        double* acc = (double*)malloc(sizeof(double) * 256);
+#pragma omp for collapse(2) schedule(dynamic)
+        for (int t = 0; t < nq; t++) {
+            for (int h = 0; h < QWO_NH; h++) {
+                const int g = h / QWO_GROUP;
+                const int64_t npos = (int64_t)pos0 + t + 1; /* causal: keys 0..pos0+t */
+                const float* qh = q + ((int64_t)t * QWO_NH + h) * 256;
+                const float* Kg = K + (int64_t)g * ld * 256;
+                const float* Vg = V + (int64_t)g * ld * 256;
+                double mx = -INFINITY;
+                for (int64_t j = 0; j < npos; j++) {
+                    const double dot = mode == 0 ? dot_exact(qh, Kg + j * 256, 256) : (double)dot_ref(qh, Kg + j * 256, 256);
+                    s[j] = dot * (1.0 / 16.0); /* softmax scale 1/sqrt(256) */
+                    if (s[j] > mx) mx = s[j];
+                }
+                double den = 0.0;
+                for (int64_t j = 0; j < npos; j++) {
+                    s[j] = exp(s[j] - mx);
+                    den += s[j];
+                }
+                for (int d = 0; d < 256; d++) acc[d] = 0.0;
+                for (int64_t j = 0; j < npos; j++) {
+                    const float* vr = Vg + j * 256;
+                    const double p = s[j];
+                    for (int d = 0; d < 256; d++) acc[d] += p * (double)vr[d];
+                }
+                const float* gh = gate + ((int64_t)t * QWO_NH + h) * 256;
+                float* o = out + ((int64_t)t * QWO_NH + h) * 256;
+                for (int d = 0; d < 256; d++) {
+                    const float a = (float)(acc[d] / den);
+                    const float sg = 1.0f / (1.0f + expf(-gh[d]));
+                    o[d] = a * sg;
+                }
+            }
+        }
+        free(s);
+        free(acc);
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * q/k prep: per-head RMSNorm * weight, NeoX RoPE on dims [0,64) in pairs (i, i+32); the angle theta^(-2i/64)*pos in
+ * double.  Follows src/cuda/ops.cu:309-358 with the double-precision arithmetic of tests/kernels/test_ops.cu:260-272.
+ * ------------------------------------------------------------------------------------------------------------- */
+static void norm_rope_row(const float* src, const float* w, const double* cs, const double* sn, float eps, float* dst) {
+    double ss = 0.0;
+    for (int d = 0; d < 256; d++) ss += (double)src[d] * (double)src[d];
+    const double sc = 1.0 / sqrt(ss / 256.0 + (double)eps);
+    double x[256];
+    for (int d = 0; d < 256; d++) x[d] = (double)src[d] * sc * (double)w[d];
+    for (int i = 0; i < 32; i++) {
+        const double x0 = x[i], x1 = x[i + 32];
+        x[i] = x0 * cs[i] - x1 * sn[i];
+        x[i + 32] = x0 * sn[i] + x1 * cs[i];
+    }
+    for (int d = 0; d < 256; d++) dst[d] = (float)x[d];
+}
+
+static void prep_token(const float* qg, const float* k, const float* q_norm, const float* k_norm, const double* cs,
+                       const double* sn, float eps, float* q_out, float* gate, float* k_out) {
+    for (int h = 0; h < QWO_NH; h++) {
+        norm_rope_row(qg + h * 512, q_norm, cs, sn, eps, q_out + h * 256);
+        memcpy(gate + h * 256, qg + h * 512 + 256, 256 * sizeof(float));
+    }
+    for (int g = 0; g < QWO_NKV; g++) norm_rope_row(k + g * 256, k_norm, cs, sn, eps, k_out + g * 256);
+}
+
+static void rope_angles(double pos, double theta, int i, double* c, double* s) {
+    const double inv = pow(theta, -2.0 * i / 64.0);
+    const double ang = fmod(pos * inv, 6.283185307179586476925286766559);
+    *c = cos(ang);
+    *s = sin(ang);
+}
+
+void qwo_attn_prep(const float* qg, const float* k, const float* q_norm, const float* k_norm, int n, int rope_pos0,
+                   float theta, float eps, float* q_out, float* gate, float* k_out) {
+    for (int r = 0; r < n; r++) {
+        double cs[32], sn[32];
+        for (int i = 0; i < 32; i++) rope_angles((double)(rope_pos0 + r), (double)theta, i, &cs[i], &sn[i]);
+        prep_token(qg + (int64_t)r * QWO_NH * 512, k + (int64_t)r * 1024, q_norm, k_norm, cs, sn, eps,
+                   q_out + (int64_t)r * 6144, gate + (int64_t)r * 6144, k_out + (int64_t)r * 1024);
+    }
+}
+
+void qwo_attn_prep_table(const float* qg, const float* k, const float* q_norm, const float* k_norm, int n,
+                         const float* rope, float eps, float* q_out, float* gate, float* k_out) {
+    for (int r = 0; r < n; r++) {
+        double cs[32], sn[32];
+        for (int i = 0; i < 32; i++) {
+            cs[i] = rope[(int64_t)r * 64 + i];
+            sn[i] = rope[(int64_t)r * 64 + 32 + i];
+        }
+        prep_token(qg + (int64_t)r * QWO_NH * 512, k + (int64_t)r * 1024, q_norm, k_norm, cs, sn, eps,
+                   q_out + (int64_t)r * 6144, gate + (int64_t)r * 6144, k_out + (int64_t)r * 1024);
+    }
+}
+
+/* src/cuda/prefill.cu:385-407 */
+void qwo_rope_table(int p0, int B, float theta, float* rope) {
+    for (int t = 0; t < B; t++)
+        for (int i = 0; i < 32; i++) {
+            double c, s;
+            rope_angles((double)(p0 + t), (double)theta, i, &c, &s);
+            rope[(int64_t)t * 64 + i] = (float)c;
+            rope[(int64_t)t * 64 + 32 + i] = (float)s;
+        }
+}
+
+void qwo_rope_table_pos(const int* pos, int B, float theta, float* rope) {
+    for (int t = 0; t < B; t++)
+        for (int i = 0; i < 32; i++) {
+            double c, s;
+            rope_angles((double)pos[t * 3 + i % 3], (double)theta, i, &c, &s);
+            rope[(int64_t)t * 64 + i] = (float)c;
+            rope[(int64_t)t * 64 + 32 + i] = (float)s;
+        }
+}
+
+/* ActQ8 epilogue, src/cuda/common.cuh:188-197: round half to even (not the KV quantizer's half-away). */
+void qwo_act_q8(const float* v, int64_t n, int8_t* q, float* d, float* s) {
+    for (int64_t b = 0; b < n / 32; b++) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) {
+            const float a = fabsf(v[32 * b + j]);
+            if (a > amax) amax = a;
+        }
+        const float db = amax / 127.0f;
+        int sum = 0;
+        for (int j = 0; j < 32; j++) {
+            const int qi = db > 0.0f ? (int)nearbyintf(v[32 * b + j] / db) : 0;
+            q[32 * b + j] = (int8_t)qi;
+            sum += qi;
+        }
+        d[b] = db;
+        s[b] = db * (float)sum;
+    }
+}
+
+int qwo_max_threads(void) { return omp_get_max_threads(); }

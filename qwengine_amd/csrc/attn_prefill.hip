@@ -1,0 +1,297 @@
+// Causal prefill attention over the quantized KV cache on fp16 MFMA (gfx950).
+//
+// FlashAttention-2 structure (the reference's k_attn_prefill_mma, src/cuda/prefill.cu:522-794, re-designed for
+// wave64 / MFMA / 160 KB LDS):
+//  * a workgroup owns 128 consecutive (query, head) rows of one KV head (row r = 6 * token + head) and walks the
+//    causal key range in 64-key tiles; its 4 waves own 32 rows each (two 16-row MFMA tiles);
+//  * every thread takes part in staging: the raw quantized K/V bytes of the next tile are loaded into registers while
+//    the current tile is computed, then dequantized to fp16 into the other half of a double buffer in LDS -- K as
+//    [key][dim], V transposed as [dim][key] so both MFMA A-operands are single 16-byte LDS reads; one barrier per tile;
+//  * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16 (fp32 accumulation); each K / V fragment read from
+//    LDS feeds both row tiles of the wave;  P^T comes out of the S^T accumulator already in B-operand layout;
+//  * online softmax in fp32 (exp2 with log2 e folded in), deferred 1/l, fused sigmoid gate, fp16 output.
+#include <float.h>
+
+#include "kv_operands.hpp"
+#include "launch.hpp"
+
+namespace qwa {
+
+constexpr int PF_WAVES = 4;
+constexpr int PF_RT = 2;                         // 16-row MFMA tiles per wave
+constexpr int PF_ROWS = PF_WAVES * PF_RT * 16;   // 128 rows per workgroup
+constexpr int PF_TILE = 64;                      // keys per tile
+constexpr int KS_LD = HD + 8;                    // K tile row stride (halves): conflict-free 16-byte reads
+constexpr int VT_LD = PF_TILE + 8;               // V^T tile row stride (halves)
+constexpr float PF_LOG2E = 1.4426950408889634f;
+
+// raw bytes of one tile held by one thread between the global load and the LDS store
+template <int KVT> struct PfRaw {
+    static constexpr int VB = value_bytes(KVT);
+    static constexpr int KP = VB / 16 / 4;          // 16-byte K pieces per thread (64 keys x VB / 16 over 256)
+    static constexpr int VW = VB / 4 / 32;          // V words per key for 8 dims
+    uint4 k[KP];
+    uint16_t ks[KP];
+    uint32_t v[8][VW];
+    uint16_t vs[8];
+};
+
+// thread t: K pieces idx = t + 256 c (key idx / P, piece idx % P); V: column block cb = t % 8 (keys of the 32-key
+// half cb / 4, lane group cb % 4), dims 8 (t / 8) .. + 8
+template <int KVT>
+__device__ __forceinline__ void pf_load(PfRaw<KVT>& r, const qwa_kv_layer& kv, size_t rowbase, int k0, int kmax) {
+    constexpr int VB = value_bytes(KVT);
+    constexpr int P = VB / 16;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < PfRaw<KVT>::KP; c++) {
+        const int idx = t + 256 * c, key = k0 + idx / P, pc = idx % P;
+        if (key <= kmax) {
+            const size_t row = rowbase + key;
+            r.k[c] = ld16(kv.k + row * VB + 16 * pc);
+            if (KVT == QWA_KV_Q4_0) r.ks[c] = kv.ks[row * 8 + pc];
+            else if (KVT == QWA_KV_Q8_0) r.ks[c] = kv.ks[row * 8 + (pc >> 1)];
+        } else {
+            r.k[c] = make_uint4(0, 0, 0, 0);
+            r.ks[c] = 0;
+        }
+    }
+    const int cb = t & 7, dc = t >> 3, h32 = cb >> 2, gq = cb & 3;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int key = k0 + 32 * h32 + (j < 4 ? 4 * gq + j : 16 + 4 * gq + (j - 4));
+        if (key <= kmax) {
+            const size_t row = rowbase + key;
+            const uint8_t* p = kv.v + row * VB + (VB / 32) * dc;
+            if constexpr (KVT == QWA_KV_Q4_0) {
+                r.v[j][0] = *reinterpret_cast<const uint32_t*>(p);
+            } else if constexpr (KVT == QWA_KV_Q8_0) {
+                const uint2 u = ld8(p);
+                r.v[j][0] = u.x; r.v[j][1] = u.y;
+            } else {
+                const uint4 u = ld16(p);
+                r.v[j][0] = u.x; r.v[j][1] = u.y; r.v[j][2] = u.z; r.v[j][3] = u.w;
+            }
+            r.vs[j] = KVT == QWA_KV_F16 ? 0 : kv.vs[row * 8 + (dc >> 2)];
+        } else {
+#pragma unroll
+            for (int i = 0; i < PfRaw<KVT>::VW; i++) r.v[j][i] = 0;
+            r.vs[j] = 0;
+        }
+    }
+}
+
+template <int KVT>
+__device__ __forceinline__ void pf_store(const PfRaw<KVT>& r, _Float16* Ks, _Float16* Vt) {
+    constexpr int VB = value_bytes(KVT);
+    constexpr int P = VB / 16;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < PfRaw<KVT>::KP; c++) {
+        const int idx = t + 256 * c, key = idx / P, pc = idx % P;
+        const uint4 u = r.k[c];
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+        if constexpr (KVT == QWA_KV_F16) {
+            *reinterpret_cast<uint4*>(Ks + key * KS_LD + 8 * pc) = u;
+        } else if constexpr (KVT == QWA_KV_Q8_0) {
+            const h2 d = scale_pair(r.ks[c], r.ks[c]);
+            uint32_t o[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) q8_word_to_h4(w[i], d, o + 2 * i);
+            *reinterpret_cast<uint4*>(Ks + key * KS_LD + 16 * pc) = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4*>(Ks + key * KS_LD + 16 * pc + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+        } else {
+            const h2 d = scale_pair(r.ks[c], r.ks[c]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t o[4];
+                q4_word_to_h8(w[i], d, o);
+                *reinterpret_cast<uint4*>(Ks + key * KS_LD + 32 * pc + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
+    }
+    const int cb = t & 7, dc = t >> 3;
+    constexpr int VW = PfRaw<KVT>::VW;
+    uint32_t pw[4][8];  // [pair][dim]
+#pragma unroll
+    for (int pr = 0; pr < 4; pr++) v_pair_words<KVT, VW>(r.v[2 * pr], r.v[2 * pr + 1], r.vs[2 * pr], r.vs[2 * pr + 1], pw[pr]);
+#pragma unroll
+    for (int d = 0; d < 8; d++)
+        *reinterpret_cast<uint4*>(Vt + (8 * dc + d) * VT_LD + 8 * cb) = make_uint4(pw[0][d], pw[1][d], pw[2][d], pw[3][d]);
+}
+
+__device__ __forceinline__ h8 lds_h8(const _Float16* p) { return *reinterpret_cast<const h8*>(p); }
+
+template <int KVT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+k_prefill(const float* __restrict__ q, const float* __restrict__ gate, qwa_kv_layer kv, int B, int p0,
+          uint16_t* __restrict__ out16) {
+    __shared__ __attribute__((aligned(16))) _Float16 s_k[2][PF_TILE * KS_LD];
+    __shared__ __attribute__((aligned(16))) _Float16 s_vt[2][HD * VT_LD];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i16 = lane & 15, lg = lane >> 4;
+    const int g = blockIdx.y;
+    const int row0 = blockIdx.x * PF_ROWS;
+    const int nrows = GRP * B;
+    // last key any row of the workgroup sees; tiles past it are never needed
+    const int last_row = min(row0 + PF_ROWS, nrows) - 1;
+    const int kmax = p0 + last_row / GRP;
+    const int n_tiles = kmax / PF_TILE + 1;
+    const size_t rowbase = (size_t)g * kv.capacity;
+
+    // this lane's rows: token tq, head hh, last visible key qpos
+    int tq[PF_RT], hh[PF_RT], qpos[PF_RT];
+    h8 qb[PF_RT][8];
+    const int wrow0 = row0 + 32 * wave;
+#pragma unroll
+    for (int rt = 0; rt < PF_RT; rt++) {
+        const int r = wrow0 + 16 * rt + i16;
+        tq[rt] = r / GRP;
+        hh[rt] = r % GRP;
+        const bool valid = tq[rt] < B;
+        qpos[rt] = valid ? p0 + tq[rt] : -1;
+        const float* qrow = q + ((size_t)(valid ? tq[rt] : 0) * NH + g * GRP + hh[rt]) * HD;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            // LDS position 32 s + 8 lg + j of a K row holds dim 32 s + 8 lg + perm(j)
+            const float* src = qrow + 32 * s + 8 * lg;
+            const float4 a = *reinterpret_cast<const float4*>(src);
+            const float4 b = *reinterpret_cast<const float4*>(src + 4);
+            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            h8 v;
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = valid ? (_Float16)(x[k_perm<KVT>(j)] * 0.0625f) : (_Float16)0.0f;
+            qb[rt][s] = v;
+        }
+    }
+    // first query of the wave: tiles entirely at or before it need no causal mask
+    const int wave_qmin = p0 + wrow0 / GRP;
+
+    f4 o[PF_RT][16];
+    float m[PF_RT], l[PF_RT];
+#pragma unroll
+    for (int rt = 0; rt < PF_RT; rt++) {
+        m[rt] = -INFINITY;
+        l[rt] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) o[rt][dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    PfRaw<KVT> raw;
+    pf_load<KVT>(raw, kv, rowbase, 0, kmax);
+    pf_store<KVT>(raw, s_k[0], s_vt[0]);
+    __syncthreads();
+
+    for (int kt = 0; kt < n_tiles; kt++) {
+        const int k0 = kt * PF_TILE, buf = kt & 1;
+        const bool more = kt + 1 < n_tiles;
+        if (more) pf_load<KVT>(raw, kv, rowbase, k0 + PF_TILE, kmax);
+        const _Float16* Ks = s_k[buf];
+        const _Float16* Vt = s_vt[buf];
+
+        // ---- S^T = K Q^T for 4 key tiles of 16
+        f4 sc[PF_RT][4];
+#pragma unroll
+        for (int k4 = 0; k4 < 4; k4++) {
+#pragma unroll
+            for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            const _Float16* kr = Ks + (16 * k4 + i16) * KS_LD + 8 * lg;
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const h8 a = lds_h8(kr + 32 * s);
+#pragma unroll
+                for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = mfma16(a, qb[rt][s], sc[rt][k4]);
+            }
+        }
+
+        // ---- mask + online softmax (lane: row (rt, i16), keys k0 + 16 k4 + 4 lg + i)
+        const bool need_mask = k0 + PF_TILE - 1 > wave_qmin;
+        h8 pb[PF_RT][2];
+#pragma unroll
+        for (int rt = 0; rt < PF_RT; rt++) {
+            float mx = -INFINITY;
+            if (need_mask) {
+#pragma unroll
+                for (int k4 = 0; k4 < 4; k4++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int key = k0 + 16 * k4 + 4 * lg + i;
+                        if (key > qpos[rt]) sc[rt][k4][i] = -INFINITY;
+                    }
+            }
+#pragma unroll
+            for (int k4 = 0; k4 < 4; k4++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[rt][k4][i]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(m[rt], mx);
+            const float msl = (mn == -INFINITY ? 0.0f : mn) * PF_LOG2E;
+            const float c = fast_exp2(m[rt] * PF_LOG2E - msl);
+            float rs = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                h8 p;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float e = fast_exp2(fmaf(sc[rt][2 * ks + (j >> 2)][j & 3], PF_LOG2E, -msl));
+                    rs += e;
+                    p[j] = (_Float16)e;
+                }
+                pb[rt][ks] = p;
+            }
+            l[rt] = l[rt] * c + rs;
+            m[rt] = mn;
+#pragma unroll
+            for (int dt = 0; dt < 16; dt++) o[rt][dt] *= c;
+        }
+
+        // ---- O^T += V^T P^T: 16 dim tiles x 2 key steps of 32
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) {
+            const _Float16* vr = Vt + (16 * dt + i16) * VT_LD + 8 * lg;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                const h8 a = lds_h8(vr + 32 * ks);
+#pragma unroll
+                for (int rt = 0; rt < PF_RT; rt++) o[rt][dt] = mfma16(a, pb[rt][ks], o[rt][dt]);
+            }
+        }
+
+        if (more) pf_store<KVT>(raw, s_k[buf ^ 1], s_vt[buf ^ 1]);
+        __syncthreads();
+    }
+
+    // ---- normalise, gate, fp16 out: lane holds dims 16 dt + 4 lg + i of row (rt, i16)
+#pragma unroll
+    for (int rt = 0; rt < PF_RT; rt++) {
+        float lt = l[rt];
+        lt += __shfl_xor(lt, 16, 64);
+        lt += __shfl_xor(lt, 32, 64);
+        if (qpos[rt] < 0) continue;
+        const float il = 1.0f / lt;
+        const size_t base = ((size_t)tq[rt] * NH + g * GRP + hh[rt]) * HD;
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) {
+            const int d = 16 * dt + 4 * lg;
+            const float4 gv = *reinterpret_cast<const float4*>(gate + base + d);
+            const float gg[4] = {gv.x, gv.y, gv.z, gv.w};
+            uint16_t hv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) hv[i] = f2h_bits(o[rt][dt][i] * il * sigmoid(gg[i]));
+            *reinterpret_cast<uint2*>(out16 + base + d) =
+                make_uint2((uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16));
+        }
+    }
+}
+
+hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
+                          uint16_t* out16, hipStream_t st) {
+    const dim3 grid((GRP * B + PF_ROWS - 1) / PF_ROWS, NKV);
+    if (kvt == QWA_KV_F16) hipLaunchKernelGGL(k_prefill<QWA_KV_F16>, grid, dim3(256), 0, st, q, gate, kv, B, p0, out16);
+    else if (kvt == QWA_KV_Q8_0) hipLaunchKernelGGL(k_prefill<QWA_KV_Q8_0>, grid, dim3(256), 0, st, q, gate, kv, B, p0, out16);
+    else hipLaunchKernelGGL(k_prefill<QWA_KV_Q4_0>, grid, dim3(256), 0, st, q, gate, kv, B, p0, out16);
+    return hipGetLastError();
+}
+
+}  // namespace qwa

@@ -1,0 +1,201 @@
+// C ABI (include/qwattn.h): argument validation, then the kernel launchers.  Nothing here allocates memory.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "launch.hpp"
+#include "qwattn_common.hpp"
+
+namespace {
+
+thread_local char g_err[256] = "";
+
+int fail(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int from_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return QWA_OK;
+    return fail(QWA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool kvt_ok(int kvt) { return kvt == QWA_KV_F16 || kvt == QWA_KV_Q8_0 || kvt == QWA_KV_Q4_0; }
+
+int check_kv(const qwa_kv_layer* kv, int kvt, const char* fn) {
+    if (!kvt_ok(kvt)) return fail(QWA_ERR_INVALID, "%s: unknown KV type %d", fn, kvt);
+    if (kv == nullptr || kv->k == nullptr || kv->v == nullptr)
+        return fail(QWA_ERR_INVALID, "%s: KV layer without value buffers", fn);
+    if (kvt != QWA_KV_F16 && (kv->ks == nullptr || kv->vs == nullptr))
+        return fail(QWA_ERR_INVALID, "%s: quantized KV layer without scale buffers", fn);
+    if (kv->capacity <= 0) return fail(QWA_ERR_INVALID, "%s: KV capacity %d", fn, kv->capacity);
+    return QWA_OK;
+}
+
+int check_src(const qwa_row_src* s, int n, const char* what, const char* fn) {
+    if (s == nullptr || (s->split > 0 && s->dev == nullptr))
+        return fail(QWA_ERR_INVALID, "%s: %s row source without device pointer", fn, what);
+    if (s->split < 0 || s->split > n) return fail(QWA_ERR_INVALID, "%s: %s split %d", fn, what, s->split);
+    if (s->split < n && s->host == nullptr)
+        return fail(QWA_ERR_INVALID, "%s: %s row source without host tail", fn, what);
+    return QWA_OK;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+size_t qwa_kv_value_bytes(int kvt) { return kvt_ok(kvt) ? (size_t)qwa::value_bytes(kvt) : 0; }
+size_t qwa_kv_scale_bytes(int kvt) { return kvt == QWA_KV_Q8_0 || kvt == QWA_KV_Q4_0 ? 16 : 0; }
+
+int qwa_attn_prep_multi(const qwa_row_src* qg, const qwa_row_src* k, const qwa_row_src* v, const float* q_norm,
+                        const float* k_norm, int pos0, int rope_pos0, int n, float theta, float eps, int kvt,
+                        const qwa_kv_layer* kv, float* q_out, float* gate, void* stream) {
+    const char* fn = "attn_prep_multi";
+    int st;
+    if ((st = check_kv(kv, kvt, fn))) return st;
+    if (n <= 0) return fail(QWA_ERR_INVALID, "%s: n = %d", fn, n);
+    if ((st = check_src(qg, 2 * qwa::NH * qwa::HD, "qg", fn)) || (st = check_src(k, qwa::NKV * qwa::HD, "k", fn)) ||
+        (st = check_src(v, qwa::NKV * qwa::HD, "v", fn)))
+        return st;
+    if (!q_norm || !k_norm || !q_out || !gate) return fail(QWA_ERR_INVALID, "%s: null pointer", fn);
+    if (pos0 < 0 || (long)pos0 + n > kv->capacity)
+        return fail(QWA_ERR_RANGE, "%s: positions [%d, %d) outside the cache capacity %d", fn, pos0, pos0 + n,
+                    kv->capacity);
+    return from_hip(qwa::launch_prep(*qg, *k, *v, q_norm, k_norm, pos0, rope_pos0, n, theta, eps, kvt, *kv, q_out,
+                                     gate, as_stream(stream)),
+                    fn);
+}
+
+int qwa_attn_prep(const float* qg, const float* k, const float* v, const float* q_norm, const float* k_norm, int pos,
+                  float theta, float eps, int kvt, const qwa_kv_layer* kv, float* q_out, float* gate, void* stream) {
+    const qwa_row_src sq{qg, nullptr, 2 * qwa::NH * qwa::HD, 0};
+    const qwa_row_src sk{k, nullptr, qwa::NKV * qwa::HD, 0};
+    const qwa_row_src sv{v, nullptr, qwa::NKV * qwa::HD, 0};
+    return qwa_attn_prep_multi(&sq, &sk, &sv, q_norm, k_norm, pos, pos, 1, theta, eps, kvt, kv, q_out, gate, stream);
+}
+
+size_t qwa_attn_work_bytes(int n_pos) {
+    if (n_pos < 1) n_pos = 1;
+    return qwa::dec_work_bytes(n_pos);
+}
+
+int qwa_attn_max_positions(void) { return qwa::MAX_POS; }
+
+int qwa_attn_decode_multi(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int pos0, int nq,
+                          void* work, float* out, const qwa_act_q8* oq, void* stream, float* out_host) {
+    const char* fn = "attn_decode_multi";
+    int st;
+    if (nq < 1 || nq > qwa::MAXQ) return fail(QWA_ERR_INVALID, "%s: %d queries (1..%d)", fn, nq, qwa::MAXQ);
+    if ((st = check_kv(kv, kvt, fn))) return st;
+    if (!q || !gate || !work || !out) return fail(QWA_ERR_INVALID, "%s: null pointer", fn);
+    if (oq && (!oq->q || !oq->d || !oq->s)) return fail(QWA_ERR_INVALID, "%s: incomplete ActQ8 output", fn);
+    if (pos0 < 0 || (long)pos0 + nq > qwa::MAX_POS)
+        return fail(QWA_ERR_RANGE, "%s: context beyond %d positions", fn, qwa::MAX_POS);
+    if ((long)pos0 + nq > kv->capacity)
+        return fail(QWA_ERR_RANGE, "%s: positions up to %d beyond the cache capacity %d", fn, pos0 + nq, kv->capacity);
+    return from_hip(qwa::launch_decode(q, gate, *kv, kvt, pos0, nq, work, out, oq, out_host, as_stream(stream)), fn);
+}
+
+int qwa_attn_decode(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int n_pos, void* work,
+                    float* out, const qwa_act_q8* oq, void* stream) {
+    if (n_pos < 1) return fail(QWA_ERR_INVALID, "attn_decode: n_pos = %d", n_pos);
+    return qwa_attn_decode_multi(q, gate, kv, kvt, n_pos - 1, 1, work, out, oq, stream, nullptr);
+}
+
+int qwa_attn_decode_simple(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int n_pos, void* work,
+                           float* out, const qwa_act_q8* oq, void* stream) {
+    const char* fn = "attn_decode_simple";
+    int st;
+    (void)work;
+    if ((st = check_kv(kv, kvt, fn))) return st;
+    if (!q || !gate || !out) return fail(QWA_ERR_INVALID, "%s: null pointer", fn);
+    if (oq && (!oq->q || !oq->d || !oq->s)) return fail(QWA_ERR_INVALID, "%s: incomplete ActQ8 output", fn);
+    if (n_pos < 1 || n_pos > kv->capacity || n_pos > qwa::MAX_POS)
+        return fail(QWA_ERR_RANGE, "%s: n_pos = %d (capacity %d)", fn, n_pos, kv->capacity);
+    return from_hip(qwa::launch_decode_simple(q, gate, *kv, kvt, n_pos, out, oq, as_stream(stream)), fn);
+}
+
+int qwa_rope_table(int p0, int B, float theta, float* rope, void* stream) {
+    if (B <= 0 || !rope || p0 < 0) return fail(QWA_ERR_INVALID, "rope_table: B = %d, p0 = %d", B, p0);
+    return from_hip(qwa::launch_rope_table(p0, B, theta, rope, as_stream(stream)), "rope_table");
+}
+
+int qwa_rope_table_pos(const int* pos3, int B, float theta, float* rope, void* stream) {
+    if (B <= 0 || !rope || !pos3) return fail(QWA_ERR_INVALID, "rope_table_pos: B = %d", B);
+    return from_hip(qwa::launch_rope_table_pos(pos3, B, theta, rope, as_stream(stream)), "rope_table_pos");
+}
+
+int qwa_attn_prep_rows(const float* qg, const float* k, const float* v, const float* q_norm, const float* k_norm,
+                       int B, int p0, const float* rope, float eps, int kvt, const qwa_kv_layer* kv, float* q,
+                       float* gate, void* stream) {
+    const char* fn = "attn_prep_rows";
+    int st;
+    if ((st = check_kv(kv, kvt, fn))) return st;
+    if (B <= 0) return fail(QWA_ERR_INVALID, "%s: B = %d", fn, B);
+    if (!qg || !k || !v || !q_norm || !k_norm || !rope || !q || !gate)
+        return fail(QWA_ERR_INVALID, "%s: null pointer", fn);
+    if (p0 < 0 || (long)p0 + B > kv->capacity)
+        return fail(QWA_ERR_RANGE, "%s: positions [%d, %d) outside the cache capacity %d", fn, p0, p0 + B,
+                    kv->capacity);
+    return from_hip(qwa::launch_prep_rows(qg, k, v, q_norm, k_norm, B, p0, rope, eps, kvt, *kv, q, gate,
+                                          as_stream(stream)),
+                    fn);
+}
+
+static int check_prefill(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
+                         uint16_t* out16, const char* fn) {
+    int st;
+    if ((st = check_kv(kv, kvt, fn))) return st;
+    if (B <= 0) return fail(QWA_ERR_INVALID, "%s: B = %d", fn, B);
+    if (!q || !gate || !out16) return fail(QWA_ERR_INVALID, "%s: null pointer", fn);
+    if (p0 < 0 || (long)p0 + B > kv->capacity || (long)p0 + B > qwa::MAX_POS)
+        return fail(QWA_ERR_RANGE, "%s: positions [%d, %d) outside the cache capacity %d", fn, p0, p0 + B,
+                    kv->capacity);
+    return QWA_OK;
+}
+
+int qwa_attn_prefill(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
+                     uint16_t* out16, void* stream) {
+    int st;
+    if ((st = check_prefill(q, gate, kv, kvt, B, p0, out16, "attn_prefill"))) return st;
+    return from_hip(qwa::launch_prefill(q, gate, *kv, kvt, B, p0, out16, as_stream(stream)), "attn_prefill");
+}
+
+int qwa_attn_prefill_simple(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
+                            uint16_t* out16, void* stream) {
+    int st;
+    if ((st = check_prefill(q, gate, kv, kvt, B, p0, out16, "attn_prefill_simple"))) return st;
+    return from_hip(qwa::launch_prefill_simple(q, gate, *kv, kvt, B, p0, out16, as_stream(stream)),
+                    "attn_prefill_simple");
+}
+
+int qwa_kv_append(const float* xk, const float* xv, int pos0, int n, int kvt, const qwa_kv_layer* kv, void* stream) {
+    const char* fn = "kv_append";
+    int st;
+    if ((st = check_kv(kv, kvt, fn))) return st;
+    if (n <= 0) return fail(QWA_ERR_INVALID, "%s: n = %d", fn, n);
+    if (!xk && !xv) return fail(QWA_ERR_INVALID, "%s: neither K nor V rows given", fn);
+    if (pos0 < 0 || (long)pos0 + n > kv->capacity)
+        return fail(QWA_ERR_RANGE, "%s: positions [%d, %d) outside the cache capacity %d", fn, pos0, pos0 + n,
+                    kv->capacity);
+    return from_hip(qwa::launch_kv_append(xk, xv, pos0, n, kvt, *kv, as_stream(stream)), fn);
+}
+
+const char* qwa_status_string(int status) {
+    switch (status) {
+        case QWA_OK: return "ok";
+        case QWA_ERR_INVALID: return "invalid argument";
+        case QWA_ERR_RANGE: return "out of range";
+        case QWA_ERR_HIP: return "HIP runtime error";
+        default: return "unknown status";
+    }
+}
+
+const char* qwa_last_error(void) { return g_err; }
+
+}  // extern "C"

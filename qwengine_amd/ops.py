@@ -1,0 +1,286 @@
+"""Host-side mirror of the reference's attention / KV-cache operators, over the C ABI of ``libqwattn.so``.
+
+Names, argument meaning and error behaviour follow ``q38rt::cuda`` (src/cuda/ops.cuh:99-140,
+src/cuda/prefill.cuh:46-62): buffers are caller-owned device tensors, every call is asynchronous on the current
+HIP stream (or ``stream=``), nothing is allocated by an operator, and an invalid call raises ``QwaError`` where the
+reference aborts.  torch is used only for device memory and streams.
+
+The HIP library must be built (``python -m qwengine_amd.build``); calls fail loudly when it is missing -- there is
+no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+F16, Q8_0, Q4_0 = 0, 1, 2
+KV_TYPES = {"f16": F16, "q8_0": Q8_0, "q4_0": Q4_0}
+N_HEAD, N_KV, HEAD_DIM, GROUP = 24, 4, 256, 6
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libqwattn.so")
+_lib = None
+
+
+class QwaError(RuntimeError):
+    """An operator rejected its arguments or a launch failed (the reference aborts in these cases)."""
+
+
+class _KVLayerC(ctypes.Structure):
+    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("ks", ctypes.c_void_p), ("vs", ctypes.c_void_p),
+                ("capacity", ctypes.c_int)]
+
+
+class _ActQ8C(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("d", ctypes.c_void_p), ("s", ctypes.c_void_p)]
+
+
+class _RowSrcC(ctypes.Structure):
+    _fields_ = [("dev", ctypes.c_void_p), ("host", ctypes.c_void_p), ("split", ctypes.c_int), ("host_ld", ctypes.c_int)]
+
+
+EXPORTS = {
+    # name: (restype, argtypes)
+    "qwa_kv_value_bytes": (ctypes.c_size_t, [ctypes.c_int]),
+    "qwa_kv_scale_bytes": (ctypes.c_size_t, [ctypes.c_int]),
+    "qwa_attn_prep": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+                                                             ctypes.POINTER(_KVLayerC), ctypes.c_void_p,
+                                                             ctypes.c_void_p, ctypes.c_void_p]),
+    "qwa_attn_prep_multi": (ctypes.c_int, [ctypes.POINTER(_RowSrcC)] * 3 + [ctypes.c_void_p] * 2 +
+                            [ctypes.c_int] * 3 + [ctypes.c_float] * 2 + [ctypes.c_int, ctypes.POINTER(_KVLayerC)] +
+                            [ctypes.c_void_p] * 3),
+    "qwa_attn_work_bytes": (ctypes.c_size_t, [ctypes.c_int]),
+    "qwa_attn_max_positions": (ctypes.c_int, []),
+    "qwa_attn_decode": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC), ctypes.c_int, ctypes.c_int,
+                                                               ctypes.c_void_p, ctypes.c_void_p,
+                                                               ctypes.POINTER(_ActQ8C), ctypes.c_void_p]),
+    "qwa_attn_decode_multi": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC)] + [ctypes.c_int] * 3 +
+                              [ctypes.c_void_p] * 2 + [ctypes.POINTER(_ActQ8C), ctypes.c_void_p, ctypes.c_void_p]),
+    "qwa_attn_decode_simple": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC), ctypes.c_int,
+                                                                      ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                                                      ctypes.POINTER(_ActQ8C), ctypes.c_void_p]),
+    "qwa_rope_table": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]),
+    "qwa_rope_table_pos": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_void_p,
+                                          ctypes.c_void_p]),
+    "qwa_attn_prep_rows": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                                                  ctypes.c_float, ctypes.c_int,
+                                                                  ctypes.POINTER(_KVLayerC)] + [ctypes.c_void_p] * 3),
+    "qwa_attn_prefill": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC)] + [ctypes.c_int] * 3 +
+                         [ctypes.c_void_p] * 2),
+    "qwa_attn_prefill_simple": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC)] +
+                                [ctypes.c_int] * 3 + [ctypes.c_void_p] * 2),
+    "qwa_kv_append": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.c_int] * 3 + [ctypes.POINTER(_KVLayerC),
+                                                                                  ctypes.c_void_p]),
+    "qwa_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "qwa_last_error": (ctypes.c_char_p, []),
+}
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def lib():
+    """Load libqwattn.so (raises if it has not been built: there is no fallback path)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise QwaError(f"HIP library missing: {_LIB_PATH} (build it with `python -m qwengine_amd.build`)")
+        L = ctypes.CDLL(_LIB_PATH)
+        for name, (res, args) in EXPORTS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        L = lib()
+        raise QwaError(f"{L.qwa_status_string(status).decode()}: {L.qwa_last_error().decode()}")
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor):
+        return int(t)
+    if not t.is_contiguous():
+        raise QwaError("tensor arguments must be contiguous")
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream if torch.cuda.is_available() else None
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    return int(stream)
+
+
+def _kvt(kvt) -> int:
+    return KV_TYPES[kvt] if isinstance(kvt, str) else int(kvt)
+
+
+def kv_value_bytes(kvt) -> int:
+    """Bytes of one 256-value head row (src/cuda/ops.cu:966-973)."""
+    return int(lib().qwa_kv_value_bytes(_kvt(kvt)))
+
+
+def kv_scale_bytes(kvt) -> int:
+    """Bytes of one row's fp16 block scales (src/cuda/ops.cu:974)."""
+    return int(lib().qwa_kv_scale_bytes(_kvt(kvt)))
+
+
+@dataclass
+class KVLayer:
+    """Per-layer KV cache in the split layout (mirror of q38rt::cuda::KVLayer, src/cuda/ops.cuh:106-113).
+
+    k, v: uint8 [4, capacity, value_bytes]; ks, vs: int16 [4, capacity, 8] fp16 bits (None for F16)."""
+    kvt: int
+    capacity: int
+    k: torch.Tensor
+    v: torch.Tensor
+    ks: torch.Tensor | None
+    vs: torch.Tensor | None
+
+    @classmethod
+    def allocate(cls, kvt, capacity: int, device="cuda", zero: bool = True) -> "KVLayer":
+        kvt = _kvt(kvt)
+        vb = kv_value_bytes(kvt)
+        alloc = torch.zeros if zero else torch.empty
+        k = alloc((N_KV, capacity, vb), dtype=torch.uint8, device=device)
+        v = alloc((N_KV, capacity, vb), dtype=torch.uint8, device=device)
+        ks = vs = None
+        if kvt != F16:
+            ks = alloc((N_KV, capacity, 8), dtype=torch.int16, device=device)
+            vs = alloc((N_KV, capacity, 8), dtype=torch.int16, device=device)
+        return cls(kvt, capacity, k, v, ks, vs)
+
+    def c(self) -> _KVLayerC:
+        return _KVLayerC(_ptr(self.k), _ptr(self.v), _ptr(self.ks), _ptr(self.vs), self.capacity)
+
+    def nbytes(self) -> int:
+        n = self.k.numel() + self.v.numel()
+        if self.ks is not None:
+            n += 2 * (self.ks.numel() + self.vs.numel())
+        return n
+
+
+@dataclass
+class ActQ8:
+    """int8 activations with per-32 scales (mirror of q38rt::cuda::ActQ8, src/cuda/gemv.cuh:14-18)."""
+    q: torch.Tensor
+    d: torch.Tensor
+    s: torch.Tensor
+
+    @classmethod
+    def allocate(cls, n: int, device="cuda") -> "ActQ8":
+        return cls(torch.empty(n, dtype=torch.int8, device=device), torch.empty(n // 32, dtype=torch.float32,
+                                                                                   device=device),
+                   torch.empty(n // 32, dtype=torch.float32, device=device))
+
+    def c(self) -> _ActQ8C:
+        return _ActQ8C(_ptr(self.q), _ptr(self.d), _ptr(self.s))
+
+
+@dataclass
+class RowSrc:
+    """Row source with a device head and an optional mapped-host tail (mirror of RowSrc, src/cuda/ops.cuh:24-34)."""
+    dev: object
+    split: int
+    host: object = None
+    host_ld: int = 0
+
+    @classmethod
+    def device(cls, t, n: int) -> "RowSrc":
+        return cls(t, n)
+
+    def c(self) -> _RowSrcC:
+        return _RowSrcC(_ptr(self.dev), _ptr(self.host), self.split, self.host_ld)
+
+
+def _act(oq):
+    return ctypes.byref(oq.c()) if oq is not None else None
+
+
+def attn_prep(qg, k, v, q_norm, k_norm, pos: int, theta: float, eps: float, kvt, kv: KVLayer, q_out, gate,
+              stream=None) -> None:
+    """src/cuda/ops.cuh:117-118."""
+    _check(lib().qwa_attn_prep(_ptr(qg), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm), pos, theta, eps, _kvt(kvt),
+                               ctypes.byref(kv.c()), _ptr(q_out), _ptr(gate), _stream(stream)))
+
+
+def attn_prep_multi(qg: RowSrc, k: RowSrc, v: RowSrc, q_norm, k_norm, pos0: int, rope_pos0: int, n: int,
+                    theta: float, eps: float, kvt, kv: KVLayer, q_out, gate, stream=None) -> None:
+    """src/cuda/ops.cuh:122-124."""
+    _check(lib().qwa_attn_prep_multi(ctypes.byref(qg.c()), ctypes.byref(k.c()), ctypes.byref(v.c()), _ptr(q_norm),
+                                     _ptr(k_norm), pos0, rope_pos0, n, theta, eps, _kvt(kvt), ctypes.byref(kv.c()),
+                                     _ptr(q_out), _ptr(gate), _stream(stream)))
+
+
+def attn_work_bytes(n_pos: int) -> int:
+    """src/cuda/ops.cuh:129."""
+    return int(lib().qwa_attn_work_bytes(n_pos))
+
+
+def attn_max_positions() -> int:
+    """src/cuda/ops.cuh:131."""
+    return int(lib().qwa_attn_max_positions())
+
+
+def attn_decode(q, gate, kv: KVLayer, kvt, n_pos: int, work, out, oq: ActQ8 | None = None, stream=None) -> None:
+    """src/cuda/ops.cuh:132-133."""
+    _check(lib().qwa_attn_decode(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), n_pos, _ptr(work), _ptr(out),
+                                 _act(oq), _stream(stream)))
+
+
+def attn_decode_multi(q, gate, kv: KVLayer, kvt, pos0: int, nq: int, work, out, oq: ActQ8 | None = None,
+                      stream=None, out_host=None) -> None:
+    """src/cuda/ops.cuh:136-137."""
+    _check(lib().qwa_attn_decode_multi(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), pos0, nq, _ptr(work),
+                                       _ptr(out), _act(oq), _stream(stream), _ptr(out_host)))
+
+
+def attn_decode_simple(q, gate, kv: KVLayer, kvt, n_pos: int, work, out, oq: ActQ8 | None = None,
+                       stream=None) -> None:
+    """src/cuda/ops.cuh:139-140."""
+    _check(lib().qwa_attn_decode_simple(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), n_pos, _ptr(work),
+                                        _ptr(out), _act(oq), _stream(stream)))
+
+
+def rope_table(p0: int, B: int, theta: float, rope, stream=None) -> None:
+    """src/cuda/prefill.cuh:46-48."""
+    _check(lib().qwa_rope_table(p0, B, theta, _ptr(rope), _stream(stream)))
+
+
+def rope_table_pos(pos, B: int, theta: float, rope, stream=None) -> None:
+    """src/cuda/prefill.cuh:49-52."""
+    _check(lib().qwa_rope_table_pos(_ptr(pos), B, theta, _ptr(rope), _stream(stream)))
+
+
+def attn_prep_rows(qg, k, v, q_norm, k_norm, B: int, p0: int, rope, eps: float, kvt, kv: KVLayer, q, gate,
+                   stream=None) -> None:
+    """src/cuda/prefill.cuh:55-56."""
+    _check(lib().qwa_attn_prep_rows(_ptr(qg), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm), B, p0, _ptr(rope), eps,
+                                    _kvt(kvt), ctypes.byref(kv.c()), _ptr(q), _ptr(gate), _stream(stream)))
+
+
+def attn_prefill(q, gate, kv: KVLayer, kvt, B: int, p0: int, out16, stream=None) -> None:
+    """src/cuda/prefill.cuh:59-60 (out16: fp16 [B, 6144])."""
+    _check(lib().qwa_attn_prefill(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), B, p0, _ptr(out16),
+                                  _stream(stream)))
+
+
+def attn_prefill_simple(q, gate, kv: KVLayer, kvt, B: int, p0: int, out16, stream=None) -> None:
+    """src/cuda/prefill.cuh:61-62."""
+    _check(lib().qwa_attn_prefill_simple(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), B, p0, _ptr(out16),
+                                         _stream(stream)))
+
+
+def kv_append(xk, xv, pos0: int, n: int, kvt, kv: KVLayer, stream=None) -> None:
+    """Quantize-on-append of raw K/V rows [n, 4, 256] (the row store of src/cuda/common.cuh:199-228)."""
+    _check(lib().qwa_kv_append(_ptr(xk), _ptr(xv), pos0, n, _kvt(kvt), ctypes.byref(kv.c()), _stream(stream)))

@@ -1,0 +1,121 @@
+"""The C ABI library (no GPU needed): it loads, exports every entry point include/qwattn.h declares, answers the
+host-only queries, and rejects invalid calls before launching anything (the reference aborts on the same inputs,
+src/cuda/ops.cu:1002-1008).  The C++ shim include/q38rt_attn.hpp compiles against it with the reference's names."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import qwengine_amd.ops as ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qwattn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qwa_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert len(names) >= 17
+    lib = ctypes.CDLL(ops.library_path())
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python mirror binds exactly those
+    assert sorted(ops.EXPORTS) == names
+
+
+def test_host_queries():
+    assert ops.kv_value_bytes("f16") == 512
+    assert ops.kv_value_bytes("q8_0") == 256
+    assert ops.kv_value_bytes("q4_0") == 128
+    assert ops.kv_value_bytes(7) == 0
+    assert ops.kv_scale_bytes("f16") == 0 and ops.kv_scale_bytes("q4_0") == 16
+    assert ops.attn_max_positions() == 262144
+    # the work buffer covers 8 queries over every 256-key split up to n_pos + 8
+    w = ops.attn_work_bytes(150000)
+    assert w >= ((150000 + 8) // 256 + 1) * 4 * 8 * 6 * 258 * 4
+    assert ops.attn_work_bytes(1) > 0
+
+
+class _Fake:
+    """A non-null 'device pointer' that is never dereferenced: every call below is rejected on the host."""
+
+    def __init__(self, v=0x1000):
+        self.v = v
+
+
+def _kv(kvt, cap=1024):
+    p = 0x10000
+    return ops.KVLayer(ops._kvt(kvt), cap, p, p, None if kvt == "f16" else p, None if kvt == "f16" else p)
+
+
+@pytest.mark.parametrize("nq", [0, 9, -1])
+def test_decode_rejects_bad_query_count(nq):
+    with pytest.raises(ops.QwaError, match="queries"):
+        ops.attn_decode_multi(0x1000, 0x1000, _kv("q8_0"), "q8_0", 10, nq, 0x1000, 0x1000)
+
+
+def test_decode_rejects_context_beyond_limits():
+    with pytest.raises(ops.QwaError, match="262144"):
+        ops.attn_decode_multi(0x1000, 0x1000, _kv("q4_0", 300000), "q4_0", 262144, 1, 0x1000, 0x1000)
+    with pytest.raises(ops.QwaError, match="capacity"):
+        ops.attn_decode_multi(0x1000, 0x1000, _kv("q4_0", 100), "q4_0", 99, 2, 0x1000, 0x1000)
+
+
+def test_rejects_bad_kv():
+    with pytest.raises(ops.QwaError, match="unknown KV type"):
+        ops.attn_decode_multi(0x1000, 0x1000, _kv("q8_0"), 5, 10, 1, 0x1000, 0x1000)
+    kv = _kv("q8_0")
+    kv.ks = None
+    with pytest.raises(ops.QwaError, match="scale"):
+        ops.attn_prefill(0x1000, 0x1000, kv, "q8_0", 4, 0, 0x1000)
+    with pytest.raises(ops.QwaError, match="capacity"):
+        ops.attn_prefill(0x1000, 0x1000, _kv("f16", 100), "f16", 64, 40, 0x1000)
+    with pytest.raises(ops.QwaError, match="B = 0"):
+        ops.attn_prefill(0x1000, 0x1000, _kv("f16", 100), "f16", 0, 0, 0x1000)
+
+
+def test_prep_rejects_bad_row_sources():
+    kv = _kv("q4_0")
+    src = ops.RowSrc(0x1000, 12288)
+    bad = ops.RowSrc(0x1000, 100)  # tail without host memory
+    with pytest.raises(ops.QwaError, match="host tail"):
+        ops.attn_prep_multi(src, bad, src, 0x1000, 0x1000, 0, 0, 1, 1e7, 1e-6, "q4_0", kv, 0x1000, 0x1000)
+    with pytest.raises(ops.QwaError, match="capacity"):
+        ops.attn_prep_multi(src, ops.RowSrc(0x1000, 1024), ops.RowSrc(0x1000, 1024), 0x1000, 0x1000, 1020, 0, 8,
+                            1e7, 1e-6, "q4_0", kv, 0x1000, 0x1000)
+
+
+def test_cpp_shim_compiles_and_links():
+    """A translation unit written against the reference's q38rt::cuda names builds against the shim + library."""
+    src = r'''
+#include "q38rt_attn.hpp"
+using namespace q38rt::cuda;
+int main() {
+    KVLayer kv; kv.capacity = 16;
+    if (kv_value_bytes(KVType::Q4_0) != 128 || kv_scale_bytes(KVType::F16) != 0) return 1;
+    if (attn_max_positions() != 262144 || attn_work_bytes(4096) == 0) return 2;
+    void (*fp)(const float*, const float*, const KVLayer&, KVType, int, int, void*, float*, const ActQ8*,
+               hipStream_t, float*) = attn_decode_multi;
+    void (*pp)(const float*, const float*, const KVLayer&, KVType, int, int, uint16_t*, hipStream_t) = attn_prefill;
+    return (fp && pp) ? 0 : 3;
+}
+'''
+    tmp = os.path.join(ROOT, "_build_test_shim")
+    os.makedirs(tmp, exist_ok=True)
+    cpp = os.path.join(tmp, "shim.cpp")
+    exe = os.path.join(tmp, "shim")
+    open(cpp, "w").write(src)
+    libdir = os.path.dirname(ops.library_path())
+    cmd = ["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"), "-I",
+           "/opt/rocm/include", cpp, "-o", exe, "-L", libdir, "-lqwattn", f"-Wl,-rpath,{libdir}"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, (r.returncode, r.stderr[-2000:])

@@ -1,0 +1,150 @@
+"""GPU parity of decode / speculative-verify attention (split-K MFMA kernel + combine) against the float64 oracle
+on the cache exactly as stored (the reference's own check, tests/kernels/test_ops.cu:288-337), the nq-independence
+contract (memcmp, test_ops.cu:244-257), the FP32 test kernel, the ActQ8 epilogue, the long-context needle test
+(test_ops.cu:354-423) and the BASELINE configurations at full size."""
+import numpy as np
+import pytest
+import torch
+
+import qwengine_amd.ops as ops
+from kvutil import KVTS, KV_NAMES, assert_close, dequant_cache, make_cache, seeded_normal
+
+pytestmark = pytest.mark.gpu
+
+
+def _qg(nq, seed):
+    return seeded_normal((nq, 24, 256), seed), seeded_normal((nq, 24, 256), seed + 100)
+
+
+def _decode(kv, q, gate, pos0, nq, oq=None):
+    work = torch.empty(ops.attn_work_bytes(pos0 + nq) // 4 + 1, dtype=torch.float32, device="cuda")
+    out = torch.empty((nq, 24, 256), device="cuda")
+    ops.attn_decode_multi(q, gate, kv, kv.kvt, pos0, nq, work, out, oq)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("kvt", KVTS, ids=lambda k: KV_NAMES[k])
+@pytest.mark.parametrize("n_pos", [1, 37, 300, 1000])
+def test_decode_vs_oracle(gpu, oracle, kvt, n_pos):
+    print(f"decode kvt={KV_NAMES[kvt]} n_pos={n_pos}", flush=True)
+    kv, _, _ = make_cache(kvt, n_pos, 1024, seed=n_pos)
+    q, gate = _qg(1, 5 + n_pos)
+    out = _decode(kv, q, gate, n_pos - 1, 1)
+    Kd, Vd = dequant_cache(kv, n_pos)
+    ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, n_pos - 1, 1)
+    assert_close(out.cpu().numpy(), ref, f"decode {KV_NAMES[kvt]} n_pos={n_pos}")
+    # the FP32 test kernel (reference tolerance 5e-5 of max |ref|, test_ops.cu:339)
+    out_s = torch.empty_like(out)
+    ops.attn_decode_simple(q, gate, kv, kvt, n_pos, None, out_s)
+    torch.cuda.synchronize()
+    err = np.abs(out_s.cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= 5e-5, err
+
+
+@pytest.mark.parametrize("kvt", KVTS, ids=lambda k: KV_NAMES[k])
+@pytest.mark.parametrize("nq", [2, 3, 5, 7, 8])
+def test_decode_multi_vs_oracle(gpu, oracle, kvt, nq):
+    pos0 = 700
+    print(f"verify kvt={KV_NAMES[kvt]} nq={nq}", flush=True)
+    kv, _, _ = make_cache(kvt, pos0 + nq, 1024, seed=nq)
+    q, gate = _qg(nq, 11 * nq)
+    out = _decode(kv, q, gate, pos0, nq)
+    Kd, Vd = dequant_cache(kv, pos0 + nq)
+    ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, pos0, nq)
+    assert_close(out.cpu().numpy(), ref, f"verify {KV_NAMES[kvt]} nq={nq}")
+
+
+@pytest.mark.parametrize("kvt", KVTS, ids=lambda k: KV_NAMES[k])
+def test_decode_multi_is_bit_identical_to_single_calls(gpu, kvt):
+    """decode_batch(n) == n x decode(), bit for bit (src/cuda/ops.cuh:134-135); split boundaries crossed on purpose."""
+    base = 509  # queries straddle the 512-key split boundary
+    kv, _, _ = make_cache(kvt, base + 8, 1024, seed=3)
+    q, gate = _qg(8, 77)
+    singles = [_decode(kv, q[t:t + 1].contiguous(), gate[t:t + 1].contiguous(), base + t, 1).cpu().numpy()
+               for t in range(8)]
+    for nq in range(1, 9):
+        for t0 in (0, 8 - nq):
+            out = _decode(kv, q[t0:t0 + nq].contiguous(), gate[t0:t0 + nq].contiguous(), base + t0, nq).cpu().numpy()
+            for t in range(nq):
+                assert np.array_equal(out[t].view(np.uint32), singles[t0 + t][0].view(np.uint32)), (nq, t0, t)
+
+
+@pytest.mark.parametrize("kvt", [ops.Q8_0, ops.Q4_0], ids=lambda k: KV_NAMES[k])
+def test_decode_actq8_epilogue(gpu, oracle, kvt):
+    nq = 3
+    kv, _, _ = make_cache(kvt, 400, 512, seed=9)
+    q, gate = _qg(nq, 123)
+    oq = ops.ActQ8.allocate(nq * 6144)
+    out = _decode(kv, q, gate, 397, nq, oq)
+    qw, dw, sw = oracle.act_q8(out.cpu().numpy())
+    assert np.array_equal(oq.q.cpu().numpy(), qw)
+    assert np.array_equal(oq.d.cpu().numpy(), dw)
+    assert np.array_equal(oq.s.cpu().numpy(), sw)
+    # the FP32 kernel's epilogue too
+    oq1 = ops.ActQ8.allocate(6144)
+    out1 = torch.empty((1, 24, 256), device="cuda")
+    ops.attn_decode_simple(q[:1].contiguous(), gate[:1].contiguous(), kv, kvt, 398, None, out1, oq1)
+    torch.cuda.synchronize()
+    qw, dw, sw = oracle.act_q8(out1.cpu().numpy())
+    assert np.array_equal(oq1.q.cpu().numpy(), qw) and np.array_equal(oq1.s.cpu().numpy(), sw)
+
+
+def test_decode_long_context_needle(gpu, oracle):
+    """140000-position Q8_0 cache with one key aligned with each group's first query at 135000
+    (tests/kernels/test_ops.cu:354-423)."""
+    n, needle, kvt = 140000, 135000, ops.Q8_0
+    q, gate = _qg(1, 2024)
+    K = seeded_normal((n, 4, 256), 31)
+    V = seeded_normal((n, 4, 256), 32)
+    K[needle] = 0.4 * q[0, ::6]
+    kv = ops.KVLayer.allocate(kvt, n)
+    ops.kv_append(K, V, 0, n, kvt, kv)
+    out = _decode(kv, q, gate, n - 1, 1)
+    Kd, Vd = dequant_cache(kv, n)
+    ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, n - 1, 1)
+    assert_close(out.cpu().numpy(), ref, "needle 140000")
+    err = np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= 2e-3  # the reference's metric and tolerance
+
+
+def test_config_c2_q8_decode_with_append(gpu, oracle):
+    """Q8_0 cache of 4096 positions, the new token's K/V quantized on append, then decode."""
+    kvt, n = ops.Q8_0, 4096
+    kv, _, _ = make_cache(kvt, n, n + 1, seed=2)
+    k_new = seeded_normal((1, 4, 256), 4242)
+    v_new = seeded_normal((1, 4, 256), 4243)
+    ops.kv_append(k_new, v_new, n, 1, kvt, kv)
+    q, gate = _qg(1, 4244)
+    out = _decode(kv, q, gate, n, 1)
+    Kd, Vd = dequant_cache(kv, n + 1)
+    # the appended rows are the oracle quantizer's, bit for bit
+    import oracle as O
+    want_v, _ = O.kv_store_rows(kvt, v_new.cpu().numpy()[0])
+    assert np.array_equal(kv.v[:, n].cpu().numpy(), want_v)
+    ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, n, 1)
+    assert_close(out.cpu().numpy(), ref, "C2")
+
+
+def test_config_c3_verify_q4_32768(gpu, oracle):
+    """7 queries (causal within the block) over a Q4_0 cache of 32768 positions."""
+    kvt, n, nq = ops.Q4_0, 32768, 7
+    kv, _, _ = make_cache(kvt, n + nq, n + nq, seed=33)
+    q, gate = _qg(nq, 3300)
+    out = _decode(kv, q, gate, n, nq)
+    Kd, Vd = dequant_cache(kv, n + nq)
+    ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, n, nq)
+    assert_close(out.cpu().numpy(), ref, "C3")
+
+
+@pytest.mark.parametrize("nq", [1, 7])
+def test_config_c5_long_decode_q4_150000(gpu, oracle, nq):
+    """150000-position Q4_0 cache, 1% of key rows x8 (outliers), 1 query and 7-query verify."""
+    kvt, n = ops.Q4_0, 150000
+    kv, _, _ = make_cache(kvt, n, n, seed=55, outlier_frac=0.01)
+    q, gate = _qg(nq, 5500 + nq)
+    pos0 = n - nq
+    out = _decode(kv, q, gate, pos0, nq)
+    Kd, Vd = dequant_cache(kv, n)
+    ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, pos0, nq)
+    assert_close(out.cpu().numpy(), ref, f"C5 nq={nq}")
