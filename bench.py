@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""Benchmark of the gated-attention hot path on one MI355X -- prints ONE JSON line.
+
+Headline (BASELINE.json metric): decode attention over a 150000-position Q4_0 KV cache, 24 query / 4 KV heads,
+head_dim 256, one query per call.  One "step" = one token's decode attention over all 16 attention layers of the
+model, each layer with its own cache (16 x 172.8 MB, so consecutive calls cannot be served from the 256 MB
+Infinity Cache).  value = algorithmic HBM bytes (150000 x 1152 B per layer) / time per layer, in GB/s.
+Secondary figures in the same line: 7-query verify at 150000 and 32768 positions, Q8_0 decode with append at 4096,
+and the 1024-token prefill chunk at p0 = 32768 (TFLOP/s against the fp16 MFMA dense peak).
+
+The CPU baseline (rank 0, N = 1 only) is the oracle's restatement of the reference CPU attention
+(src/reference/ref_model.cpp:195-219: fp32 8-lane FMA dots, double softmax, OpenMP over (token, head)) on a bounded
+sample of the same workload, timed on this box's host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+METRIC = "decode attn µs/layer + HBM GB/s @150K Q4_0 KV; prefill attn TFLOP/s (1024-tok chunk)"
+BYTES_PER_POS = {0: 4096, 1: 2176, 2: 1152}  # K + V values and scales over the 4 KV heads
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=16)
+    ap.add_argument("--positions", type=int, default=150000)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="headline decode only")
+    return ap.parse_args()
+
+
+def fill_cache(ops, torch, kvt, n, seed, outlier_frac=0.01):
+    kv = ops.KVLayer.allocate(kvt, n, zero=False)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    chunk = 32768
+    for p in range(0, n, chunk):
+        m = min(chunk, n - p)
+        K = torch.randn((m, 4, 256), generator=g, device="cuda")
+        V = torch.randn((m, 4, 256), generator=g, device="cuda")
+        if outlier_frac:
+            K[torch.rand((m, 4), generator=g, device="cuda") < outlier_frac] *= 8.0
+        ops.kv_append(K, V, p, m, kvt, kv)
+    return kv
+
+
+def time_calls(torch, fn, reps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps  # ms
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the path has no multi-GPU "
+              "collective -- run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import qwengine_amd.ops as ops
+
+    ops.lib()
+    torch.manual_seed(0)
+    n, L = args.positions, args.layers
+    kvt = ops.Q4_0
+    print(f"[bench] filling {L} layer caches of {n} Q4_0 positions", file=sys.stderr, flush=True)
+    layers = [fill_cache(ops, torch, kvt, n, 1000 + i) for i in range(L)]
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn((8, 24, 256), generator=g, device="cuda")
+    gate = torch.randn((8, 24, 256), generator=g, device="cuda")
+    work = torch.empty(ops.attn_work_bytes(n) // 4 + 1, dtype=torch.float32, device="cuda")
+    out = torch.empty((8, 24, 256), device="cuda")
+
+    def step(nq=1):
+        for kv in layers:
+            ops.attn_decode_multi(q, gate, kv, kvt, n - nq, nq, work, out)
+
+    # ---- headline: W warmup steps, then exactly K timed steps
+    print(f"[bench] decode: {args.warmup} warmup + {args.steps} timed steps", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    us_layer = ms_per_step * 1000.0 / L
+    bytes_layer = n * BYTES_PER_POS[kvt]
+    gbs = bytes_layer / (us_layer * 1e-6) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (K/V ~N(0,1), 1% of key rows x8, quantized on append; random gate logits)",
+        "config": {"workload": "decode_q4_0_150k", "kv": "q4_0", "positions": n, "queries_per_call": 1,
+                   "layers_per_step": L, "q_heads": 24, "kv_heads": 4, "head_dim": 256},
+        "decode_us_per_layer": round(us_layer, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "attn_decode_multi call (k_dec + k_dec_combine), per-layer launch average",
+                     "algorithmic_bytes_per_launch": bytes_layer},
+    }
+
+    if not args.no_extra:
+        extra = {}
+        # 7-query speculative verify over the same 150000-position caches
+        ms = time_calls(torch, lambda: step(7), max(5, args.steps // 5), 2)
+        us = ms * 1000.0 / L
+        extra["verify7_150k_us_per_layer"] = round(us, 3)
+        extra["verify7_150k_gbs"] = round((n + 6) * BYTES_PER_POS[kvt] / (us * 1e-6) / 1e9, 1)
+        del layers
+        torch.cuda.empty_cache()
+        # C3: 7-query verify over Q4_0 32768 (16 layers)
+        n3 = 32768 + 7
+        l3 = [fill_cache(ops, torch, ops.Q4_0, n3, 2000 + i) for i in range(L)]
+        ms = time_calls(torch, lambda: [ops.attn_decode_multi(q, gate, kv, ops.Q4_0, 32768, 7, work, out) for kv in l3],
+                        max(5, args.steps // 5), 2)
+        us = ms * 1000.0 / L
+        extra["verify7_q4_32768_us_per_layer"] = round(us, 3)
+        extra["verify7_q4_32768_gbs"] = round(n3 * 1152 / (us * 1e-6) / 1e9, 1)
+        del l3
+        # C2: Q8_0 4096 decode with the new token's quantize-on-append (append + decode per layer)
+        l2 = [fill_cache(ops, torch, ops.Q8_0, 4097, 3000 + i, 0.0) for i in range(L)]
+        knew = torch.randn((1, 4, 256), device="cuda")
+        vnew = torch.randn((1, 4, 256), device="cuda")
+
+        def c2():
+            for kv in l2:
+                ops.kv_append(knew, vnew, 4096, 1, ops.Q8_0, kv)
+                ops.attn_decode_multi(q, gate, kv, ops.Q8_0, 4096, 1, work, out)
+        ms = time_calls(torch, c2, max(5, args.steps // 5), 2)
+        extra["decode_q8_4096_append_us_per_layer"] = round(ms * 1000.0 / L, 3)
+        del l2
+        # C4: prefill chunk of 1024 tokens at p0 = 32768, Q8_0
+        p0, B = 32768, 1024
+        kv4 = fill_cache(ops, torch, ops.Q8_0, p0 + B, 4000, 0.0)
+        qp = torch.randn((B, 24, 256), device="cuda").half().float()
+        gp = torch.randn((B, 24, 256), device="cuda")
+        o16 = torch.empty((B, 24, 256), dtype=torch.float16, device="cuda")
+        ms = time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 10, 2)
+        flop = 4.0 * 24 * 256 * sum(p0 + t + 1 for t in range(B))
+        tflops = flop / (ms * 1e-3) / 1e12
+        extra["prefill_1024_at_32768_ms"] = round(ms, 4)
+        extra["prefill_tflops"] = round(tflops, 1)
+        extra["prefill_mfma_frac"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
+        result["extra"] = extra
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(ops, torch, n)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(ops, torch, n):
+    """The reference CPU arithmetic (oracle mode 1) on one layer of the headline workload, host threads."""
+    import numpy as np
+    import oracle as O
+    sys.path.insert(0, os.path.join(HERE, "tests"))
+    print("[bench] cpu baseline", file=sys.stderr, flush=True)
+    kv = fill_cache(ops, torch, ops.Q4_0, n, 1000)
+    K = O.kv_load_rows(ops.Q4_0, kv.k.cpu().numpy(), kv.ks.cpu().numpy().view(np.uint16))
+    V = O.kv_load_rows(ops.Q4_0, kv.v.cpu().numpy(), kv.vs.cpu().numpy().view(np.uint16))
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((1, 24, 256)).astype(np.float32)
+    g = rng.standard_normal((1, 24, 256)).astype(np.float32)
+    threads = O.max_threads()
+    O.attention(q, g, K, V, n - 1, 1, mode=1)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < 10.0:
+        O.attention(q, g, K, V, n - 1, 1, mode=1)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    us = dt * 1e6
+    return {"value": round(n * 1152 / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_layer": round(us, 1),
+            "sample": f"{reps} decode calls over one 150000-position Q4_0 layer (cache dequantized to fp32), "
+                      f"oracle mode 1 = reference CPU arithmetic, {threads} OpenMP threads"}
+
+
+if __name__ == "__main__":
+    main()

@@ -4,9 +4,10 @@
 //  * rows are (query, head) pairs of one KV head, row r = 6 * query + head, in 16-row MFMA tiles
 //    (RT = ceil(6 nq / 16) tiles); a wave owns one fixed 256-key split x one row tile, and the RT waves of a split
 //    sit in the same workgroup so their K/V reads share L1 / L2;
-//  * 16-key chunks: S^T = K Q^T on v_mfma_f32_16x16x32_f16 and O^T = V^T P^T on v_mfma_f32_16x16x16_f16, fp32
-//    accumulation, Q pre-scaled by 1/16 (exact in fp16); K and V are read straight from HBM with 8/16-byte loads
-//    and dequantized in registers; with S^T in the accumulator a lane holds 4 keys of ONE row, so the online
+//  * 16-key chunks: S = Q K^T on v_mfma_f32_16x16x32_f16 (one MFMA per 32-dim quant block, exact integer K codes,
+//    fp32 block-scale applied to the partial dots, Q / 16 as fp16 hi + lo) and O^T = V^T P^T on
+//    v_mfma_f32_16x16x16_f16 (V dequantized to fp16 in registers), fp32 accumulation; K and V are read straight
+//    from HBM; the 16 x 16 score tile is transposed through LDS so that a lane holds 4 keys of ONE row: the online
 //    softmax is lane-local up to a 4-lane max / sum, and P^T is already the B operand of the P.V product;
 //  * a ring of NBUF chunks per wave keeps loads in flight while the current chunk is computed;
 //  * each split writes a partial record (m, l, O[256]); k_dec_combine merges them in a fixed order, normalises,
@@ -31,19 +32,53 @@ size_t dec_work_bytes(int n_pos) {
     return mma;
 }
 
-// Raw bytes of one 16-key chunk held by one lane: K of key kb + (lane % 16) (dims 64 g .. 64 g + 63) and V of keys
-// kb + 4 g + j, j = 0..3 (dims 16 (lane % 16) .. + 15).
+// Raw bytes of one 16-key chunk held by one lane.
+//  K (B operand of S = Q K^T, one MFMA per 32-dim quant block): key kb + (lane % 16), for every block b the 8 dims
+//    32 b + 8 g + perm(j) as raw bytes (Q4_0: 1 word per block, Q8_0: 2, F16: 4), plus that key's 8 block scales.
+//  V (A operand of O^T = V^T P^T): keys kb + 4 g + j, j = 0..3, dims 16 (lane % 16) .. + 15, with their scales.
+template <int KVT> struct KChunk;
+template <> struct KChunk<QWA_KV_Q4_0> { uint32_t w[8]; uint32_t sc[4]; };
+template <> struct KChunk<QWA_KV_Q8_0> { uint32_t w[16]; uint32_t sc[4]; };
+template <> struct KChunk<QWA_KV_F16> { uint32_t w[32]; uint32_t sc[4]; };
+
 template <int KVT>
 struct Chunk {
-    KRaw<KVT> k;
+    KChunk<KVT> k;
     VRaw<KVT> v[4];
 };
 
 template <int KVT>
 __device__ __forceinline__ void load_chunk(Chunk<KVT>& c, const qwa_kv_layer& kv, size_t rowbase, int kb, int kmax,
                                            int i16, int lg) {
+    constexpr int VB = value_bytes(KVT);
+    constexpr int WPB = sizeof(c.k.w) / 4 / 8;  // raw words per block per lane
     const int key = kb + i16;
-    load_k<KVT>(c.k, kv, rowbase + key, lg, key <= kmax);
+    if (key <= kmax) {
+        const size_t row = rowbase + key;
+        const uint8_t* p = kv.k + row * VB + 4 * WPB * lg;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const uint8_t* pb = p + (VB / 8) * b;
+            if constexpr (WPB == 1) {
+                c.k.w[b] = *reinterpret_cast<const uint32_t*>(pb);
+            } else if constexpr (WPB == 2) {
+                const uint2 u = ld8(pb);
+                c.k.w[2 * b] = u.x; c.k.w[2 * b + 1] = u.y;
+            } else {
+                const uint4 u = ld16(pb);
+                c.k.w[4 * b] = u.x; c.k.w[4 * b + 1] = u.y; c.k.w[4 * b + 2] = u.z; c.k.w[4 * b + 3] = u.w;
+            }
+        }
+        if constexpr (KVT != QWA_KV_F16) {
+            const uint4 u = *reinterpret_cast<const uint4*>(kv.ks + row * 8);
+            c.k.sc[0] = u.x; c.k.sc[1] = u.y; c.k.sc[2] = u.z; c.k.sc[3] = u.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8 * WPB; i++) c.k.w[i] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) c.k.sc[i] = 0;
+    }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int vk = kb + 4 * lg + j;
@@ -51,40 +86,76 @@ __device__ __forceinline__ void load_chunk(Chunk<KVT>& c, const qwa_kv_layer& kv
     }
 }
 
+// B operand of block b: exact integers (no scale), dims 32 b + 8 g + perm(j)
+template <int KVT>
+__device__ __forceinline__ h8 k_block_int(const KChunk<KVT>& k, int b) {
+    if constexpr (KVT == QWA_KV_F16) {
+        return make_h8(k.w[4 * b], k.w[4 * b + 1], k.w[4 * b + 2], k.w[4 * b + 3]);
+    } else if constexpr (KVT == QWA_KV_Q8_0) {
+        uint32_t o[4];
+        q8_word_int(k.w[2 * b], o);
+        q8_word_int(k.w[2 * b + 1], o + 2);
+        return make_h8(o[0], o[1], o[2], o[3]);
+    } else {
+        uint32_t o[4];
+        q4_word_int(k.w[b], o);
+        return make_h8(o[0], o[1], o[2], o[3]);
+    }
+}
+
 __device__ __forceinline__ f4 mfma16k16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
 // One wave = one 256-key split x one 16-row tile.  Workgroup = SPW splits x RT row tiles (waves of the same split
 // share the K/V lines through L1 / L2).  NBUF chunks are in flight per wave (register ring).
+//
+// Scores are exact up to fp32 accumulation: K enters the MFMA as the exact integer codes and its fp16 block scale is
+// applied to each block's fp32 partial dot (one MFMA per 32-dim block); Q / 16 is split into fp16 hi + lo parts
+// (two MFMAs), i.e. ~22 significant bits.  This keeps large (outlier) logits within tolerance where fp16(Q) and
+// fp16(d * x) would not.
 template <int KVT, int RT, int SPW, int NBUF>
-__global__ void __launch_bounds__(64 * RT * SPW) __attribute__((amdgpu_waves_per_eu(2, 2))) k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq,
-                                                       int nsplit, float* __restrict__ work) {
+__global__ void __launch_bounds__(64 * RT * SPW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int nsplit, float* __restrict__ work) {
+    // Q / 16 hi and lo parts in A-operand order: [rt][block][hi, lo][lane] x 8 halves (16 KB per row tile)
+    __shared__ h8 s_q[RT][8][2][64];
+    __shared__ float s_t[RT * SPW][16][20];  // per-wave transpose of the 16 x 16 score tile
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i16 = lane & 15, lg = lane >> 4;
+    const int g = blockIdx.y;
+    const int kmax = pos0 + nq - 1;
+
+    for (int e = threadIdx.x; e < RT * 8 * 64; e += 64 * RT * SPW) {
+        const int rt = e >> 9, b = (e >> 6) & 7, ln = e & 63;
+        const int r = 16 * rt + (ln & 15);
+        const int qt = r / GRP, hh = r % GRP;
+        h8 hi, lo;
+        if (qt < nq) {
+            const float* src = q + ((size_t)qt * NH + g * GRP + hh) * HD + 32 * b + 8 * (ln >> 4);
+            const float4 a = *reinterpret_cast<const float4*>(src);
+            const float4 c = *reinterpret_cast<const float4*>(src + 4);
+            const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float v = x[k_perm<KVT>(j)] * 0.0625f;
+                hi[j] = (_Float16)v;
+                lo[j] = (_Float16)(v - (float)hi[j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) hi[j] = lo[j] = (_Float16)0.0f;
+        }
+        s_q[rt][b][0][ln] = hi;
+        s_q[rt][b][1][ln] = lo;
+    }
+    __syncthreads();
+
     const int split = blockIdx.x * SPW + wave / RT;
     const int rt = wave % RT;
     if (split >= nsplit) return;
-    const int g = blockIdx.y;
-    const int i16 = lane & 15, lg = lane >> 4;
-    const int kmax = pos0 + nq - 1;
-
-    // this lane's row: query qt, head hh, last visible key qpos (-1: padding row)
+    // this lane's row in the S^T layout: query qt, head hh, last visible key qpos (-1: padding row)
     const int r = 16 * rt + i16;
     const int qt = r / GRP, hh = r % GRP;
-    const bool valid = qt < nq;
-    const int qpos = valid ? pos0 + qt : -1;
-    h8 qb[8];
-    {
-        const float* qrow = q + ((size_t)(valid ? qt : 0) * NH + g * GRP + hh) * HD + 64 * lg;
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const float4 a = *reinterpret_cast<const float4*>(qrow + 8 * s);
-            const float4 b = *reinterpret_cast<const float4*>(qrow + 8 * s + 4);
-            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            h8 v;
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = valid ? (_Float16)(x[k_perm<KVT>(j)] * 0.0625f) : (_Float16)0.0f;
-            qb[s] = v;
-        }
-    }
+    const int qpos = qt < nq ? pos0 + qt : -1;
+    float (*tr)[20] = s_t[wave];
 
     f4 o[16];
 #pragma unroll
@@ -101,26 +172,40 @@ __global__ void __launch_bounds__(64 * RT * SPW) __attribute__((amdgpu_waves_per
 
     for (int kb0 = k_begin; kb0 < k_end; kb0 += 16 * NBUF) {
 #pragma unroll
-        for (int b = 0; b < NBUF; b++) {
-            const int kb = kb0 + 16 * b;
+        for (int bi = 0; bi < NBUF; bi++) {
+            const int kb = kb0 + 16 * bi;
             if (kb >= k_end) break;
-            const Chunk<KVT>& c = buf[b];
+            const Chunk<KVT>& c = buf[bi];
 
-            // ---- S^T = K Q^T (16 keys x 16 rows), two accumulation chains
-            f4 s0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+            // ---- S = Q K^T (16 rows x 16 keys): per block, (Q_hi + Q_lo) . K_int, scaled by the key's block scale
+            f4 S = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int s = 0; s < 8; s += 2) {
-                s0 = mfma16(k_operand<KVT>(c.k, s), qb[s], s0);
-                s1 = mfma16(k_operand<KVT>(c.k, s + 1), qb[s + 1], s1);
+            for (int b = 0; b < 8; b++) {
+                const h8 kb8 = k_block_int<KVT>(c.k, b);
+                f4 a = mfma16(s_q[rt][b][0][lane], kb8, f4{0.0f, 0.0f, 0.0f, 0.0f});
+                a = mfma16(s_q[rt][b][1][lane], kb8, a);
+                if constexpr (KVT == QWA_KV_F16) {
+                    S += a;
+                } else {
+                    const float d = h2f_bits((uint16_t)(c.k.sc[b >> 1] >> (16 * (b & 1))));
+#pragma unroll
+                    for (int i = 0; i < 4; i++) S[i] = fmaf(d, a[i], S[i]);
+                }
             }
-            const f4 sc = s0 + s1;
+            // lane (key i16, g) holds rows 4 g + i -> transpose through LDS to lane (row i16, g) holding keys 4 g + i
+#pragma unroll
+            for (int i = 0; i < 4; i++) tr[4 * lg + i][i16] = S[i];
+            __builtin_amdgcn_wave_barrier();
+            const float4 st = *reinterpret_cast<const float4*>(&tr[i16][4 * lg]);
+            __builtin_amdgcn_wave_barrier();
 
             // ---- causal mask + online softmax: lane holds keys kb + 4 lg + i of its row
+            const float sc4[4] = {st.x, st.y, st.z, st.w};
             float sv[4];
             float mx = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                sv[i] = kb + 4 * lg + i <= qpos ? sc[i] : -INFINITY;
+                sv[i] = kb + 4 * lg + i <= qpos ? sc4[i] : -INFINITY;
                 mx = fmaxf(mx, sv[i]);
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -161,7 +246,7 @@ __global__ void __launch_bounds__(64 * RT * SPW) __attribute__((amdgpu_waves_per
 
             // ---- refill this slot with the chunk NBUF ahead
             const int kn = kb + 16 * NBUF;
-            if (kn < k_end) load_chunk<KVT>(buf[b], kv, rowbase, kn, kmax, i16, lg);
+            if (kn < k_end) load_chunk<KVT>(buf[bi], kv, rowbase, kn, kmax, i16, lg);
         }
     }
 

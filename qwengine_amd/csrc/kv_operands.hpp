@@ -93,6 +93,20 @@ __device__ __forceinline__ h8 k_operand(const KRaw<KVT>& r, int s) {
     }
 }
 
+// Exact small integers as fp16 (no scale): the codes c - 8 of a Q4_0 word in the k_operand order, or the int8
+// values of a Q8_0 word.
+__device__ __forceinline__ void q4_word_int(uint32_t w, uint32_t* out) {
+    const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+#pragma unroll
+    for (int k = 0; k < 4; k++) out[k] = h2_bits(bits_h2(((w >> (4 * k)) & 0x000F000Fu) | 0x64006400u) - bias);
+}
+__device__ __forceinline__ void q8_word_int(uint32_t w, uint32_t* out) {
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t u = w ^ 0x80808080u;
+    out[0] = h2_bits(bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x05010400u)) - bias);
+    out[1] = h2_bits(bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x05030402u)) - bias);
+}
+
 // Position of dim j inside the 8-dim group a K operand lane holds (see k_operand).
 template <int KVT>
 __device__ __forceinline__ constexpr int k_perm(int j) {
