@@ -1,20 +1,25 @@
 // Decode / speculative-verify attention over the quantized KV cache (gfx950).
 //
-// Split-K flash-decoding (the reference's structure, src/cuda/ops.cu:507-815, re-designed for wave64 + MFMA):
-//  * rows are (query, head) pairs of one KV head, row r = 6 * query + head, in 16-row MFMA tiles
-//    (RT = ceil(6 nq / 16) tiles); a wave owns one fixed 256-key split x one row tile, and the RT waves of a split
-//    sit in the same workgroup so their K/V reads share L1 / L2;
-//  * 16-key chunks: S = Q K^T on v_mfma_f32_16x16x32_f16 (one MFMA per 32-dim quant block, exact integer K codes,
-//    fp32 block-scale applied to the partial dots, Q / 16 as fp16 hi + lo) and O^T = V^T P^T on
-//    v_mfma_f32_16x16x16_f16 (V dequantized to fp16 in registers), fp32 accumulation; K and V are read straight
-//    from HBM; the 16 x 16 score tile is transposed through LDS so that a lane holds 4 keys of ONE row: the online
-//    softmax is lane-local up to a 4-lane max / sum, and P^T is already the B operand of the P.V product;
-//  * a ring of NBUF chunks per wave keeps loads in flight while the current chunk is computed;
-//  * each split writes a partial record (m, l, O[256]); k_dec_combine merges them in a fixed order, normalises,
-//    applies the sigmoid gate and the optional ActQ8 epilogue.
-// Split boundaries are fixed multiples of 256 keys and masked keys contribute exact zeros, so a query's output does
-// not depend on how many queries share the call (the reference's decode == decode_batch contract,
-// src/cuda/ops.cuh:134-135).
+// Split-K flash-decoding (the reference's structure, src/cuda/ops.cu:507-815, re-designed for wave64 + MFMA and for
+// streaming HBM at full rate):
+//  * the keys of a KV head are cut into 16-key chunks; chunk c belongs to class c mod DEC_CLASSES (512 classes per
+//    head, a fixed function of the chunk index); a wave owns one class and walks its chunks in increasing order, so
+//    at any moment all waves of the chip stream neighbouring chunks (grid-stride locality) and a 150000-position
+//    head gives every wave ~18 chunks (2048 waves = 2 per SIMD);
+//  * chunks are fetched with direct-to-LDS loads (global_load_lds, 16 B per lane) into an NST-stage per-wave ring;
+//    each lane's source piece is rotated per row so the MFMA operand reads from LDS are (nearly) bank-conflict free;
+//  * rows are (query, head) pairs of one KV head, row r = 6 * query + head, in RT 16-row MFMA tiles;
+//    S^T = K Q^T on v_mfma_f32_16x16x32_f16, one MFMA per 32-dim quant block with the exact integer K codes and
+//    Q / 16 as fp16 hi + lo parts, the key's fp16 block scale applied to each block's fp32 partial dot (scores exact
+//    up to fp32 accumulation, so outlier logits stay within tolerance); a lane then holds 4 keys of ONE row: the
+//    online softmax is lane-local up to a 4-lane max / sum, and P^T is directly the B operand of
+//    O^T += V^T P^T (v_mfma_f32_16x16x16_f16, V dequantized to fp16 in registers, fp32 accumulation);
+//  * the 4 classes of a workgroup are merged as fold(fold(c0, c1), fold(c2, c3)) into one partial record
+//    (m, l, O[256]) per row; k_dec_combine merges the records in a fixed order, normalises, applies the sigmoid gate
+//    and the optional ActQ8 epilogue.
+// Every reduction runs over a partition of the keys that depends only on key indices, and masked keys contribute
+// exact zeros, so a query's output does not depend on how many queries share the call (the reference's
+// decode == decode_batch contract, src/cuda/ops.cuh:134-135).
 #include <float.h>
 
 #include "kv_operands.hpp"
@@ -22,110 +27,156 @@
 
 namespace qwa {
 
-constexpr int REC = 260;   // partial record: m, l, 2 pad, O[256] (16-byte aligned O)
-constexpr int CGRP = 32;   // combine: splits per fixed summation group
+constexpr int REC = 260;    // partial record: m, l, 2 pad, O[256] (16-byte aligned O)
+constexpr int CGRP = 16;    // combine: records per fixed summation group
+constexpr int CHUNK = 16;   // keys per chunk
+constexpr int WG_CLASSES = 4;
+constexpr int NREC = DEC_CLASSES / WG_CLASSES;  // records (workgroups) per KV head
 constexpr float LOG2E = 1.4426950408889634f;
 
 size_t dec_work_bytes(int n_pos) {
-    const size_t nsplit = (size_t)dec_nsplit(n_pos + MAXQ);
-    const size_t mma = nsplit * NKV * MAXQ * GRP * REC * sizeof(float);
-    return mma;
+    (void)n_pos;
+    return (size_t)NREC * NKV * MAXQ * GRP * REC * sizeof(float);
 }
 
-// Raw bytes of one 16-key chunk held by one lane.
-//  K (B operand of S = Q K^T, one MFMA per 32-dim quant block): key kb + (lane % 16), for every block b the 8 dims
-//    32 b + 8 g + perm(j) as raw bytes (Q4_0: 1 word per block, Q8_0: 2, F16: 4), plus that key's 8 block scales.
-//  V (A operand of O^T = V^T P^T): keys kb + 4 g + j, j = 0..3, dims 16 (lane % 16) .. + 15, with their scales.
-template <int KVT> struct KChunk;
-template <> struct KChunk<QWA_KV_Q4_0> { uint32_t w[8]; uint32_t sc[4]; };
-template <> struct KChunk<QWA_KV_Q8_0> { uint32_t w[16]; uint32_t sc[4]; };
-template <> struct KChunk<QWA_KV_F16> { uint32_t w[32]; uint32_t sc[4]; };
-
+// one 16-key chunk in LDS: K rows, V rows (VB bytes each, 16-byte pieces rotated by the row index), block scales
 template <int KVT>
-struct Chunk {
-    KChunk<KVT> k;
-    VRaw<KVT> v[4];
+struct ChunkLds {
+    static constexpr int VB = value_bytes(KVT);
+    static constexpr int PIECES = VB / 16;  // 16-byte pieces per row
+    static constexpr int KBYTES = CHUNK * VB;
+    static constexpr int SC = KVT == QWA_KV_F16 ? 0 : CHUNK * 16;
+    static constexpr int BYTES = 2 * KBYTES + 2 * SC;
+    static constexpr int NLOAD = 2 * KBYTES / 1024 + (SC ? 2 : 0);  // load instructions per chunk
 };
 
+// LDS offset of byte `byte` (< VB) of row `row` (pieces rotated by row)
 template <int KVT>
-__device__ __forceinline__ void load_chunk(Chunk<KVT>& c, const qwa_kv_layer& kv, size_t rowbase, int kb, int kmax,
-                                           int i16, int lg) {
-    constexpr int VB = value_bytes(KVT);
-    constexpr int WPB = sizeof(c.k.w) / 4 / 8;  // raw words per block per lane
-    const int key = kb + i16;
-    if (key <= kmax) {
-        const size_t row = rowbase + key;
-        const uint8_t* p = kv.k + row * VB + 4 * WPB * lg;
+__device__ __forceinline__ int rot_off(int row, int byte) {
+    constexpr int VB = ChunkLds<KVT>::VB, P = ChunkLds<KVT>::PIECES;
+    return row * VB + 16 * (((byte >> 4) + row) % P) + (byte & 15);
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Issue the direct-to-LDS loads of chunk `kb` (rows past klim re-read row klim: no branch, no read outside the
+// window; their scores are masked and their probabilities are exact zeros).
+template <int KVT>
+__device__ __forceinline__ void issue_chunk(uint8_t* dst, const qwa_kv_layer& kv, size_t rowbase, int kb, int klim,
+                                            int lane) {
+    using C = ChunkLds<KVT>;
+    constexpr int VB = C::VB, P = C::PIECES;
 #pragma unroll
-        for (int b = 0; b < 8; b++) {
-            const uint8_t* pb = p + (VB / 8) * b;
-            if constexpr (WPB == 1) {
-                c.k.w[b] = *reinterpret_cast<const uint32_t*>(pb);
-            } else if constexpr (WPB == 2) {
-                const uint2 u = ld8(pb);
-                c.k.w[2 * b] = u.x; c.k.w[2 * b + 1] = u.y;
-            } else {
-                const uint4 u = ld16(pb);
-                c.k.w[4 * b] = u.x; c.k.w[4 * b + 1] = u.y; c.k.w[4 * b + 2] = u.z; c.k.w[4 * b + 3] = u.w;
-            }
-        }
-        if constexpr (KVT != QWA_KV_F16) {
-            const uint4 u = *reinterpret_cast<const uint4*>(kv.ks + row * 8);
-            c.k.sc[0] = u.x; c.k.sc[1] = u.y; c.k.sc[2] = u.z; c.k.sc[3] = u.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8 * WPB; i++) c.k.w[i] = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) c.k.sc[i] = 0;
+    for (int i = 0; i < C::KBYTES / 1024; i++) {
+        // LDS slot (row, s) <- global piece (s - row) mod P of that row
+        const int slot = lane + 64 * i, row = slot / P, s = slot % P;
+        const int piece = (s - row % P + P) % P;
+        const size_t grow = rowbase + min(kb + row, klim);
+        __builtin_amdgcn_global_load_lds(kv.k + grow * VB + 16 * piece, (lds_void*)(dst + 1024 * i), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(kv.v + grow * VB + 16 * piece, (lds_void*)(dst + C::KBYTES + 1024 * i), 16,
+                                         0, 0);
     }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int vk = kb + 4 * lg + j;
-        load_v<KVT>(c.v[j], kv, rowbase + vk, i16, vk <= kmax);
+    if constexpr (C::SC) {
+        const size_t grow = rowbase + min(kb + lane / 4, klim);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(kv.ks + grow * 8) + 4 * (lane & 3),
+                                         (lds_void*)(dst + 2 * C::KBYTES), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(kv.vs + grow * 8) + 4 * (lane & 3),
+                                         (lds_void*)(dst + 2 * C::KBYTES + C::SC), 4, 0, 0);
     }
 }
 
-// B operand of block b: exact integers (no scale), dims 32 b + 8 g + perm(j)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// A operand of block b for lane (key n, group g): exact integers (no scale), dims 32 b + 8 g + perm(j)
 template <int KVT>
-__device__ __forceinline__ h8 k_block_int(const KChunk<KVT>& k, int b) {
+__device__ __forceinline__ h8 k_block_int(const uint8_t* kst, int n, int g, int b) {
+    constexpr int VB = ChunkLds<KVT>::VB;
+    const uint8_t* p = kst + rot_off<KVT>(n, (VB / 8) * b + (VB / 32) * g);
     if constexpr (KVT == QWA_KV_F16) {
-        return make_h8(k.w[4 * b], k.w[4 * b + 1], k.w[4 * b + 2], k.w[4 * b + 3]);
+        return *reinterpret_cast<const h8*>(p);
     } else if constexpr (KVT == QWA_KV_Q8_0) {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
         uint32_t o[4];
-        q8_word_int(k.w[2 * b], o);
-        q8_word_int(k.w[2 * b + 1], o + 2);
+        q8_word_int(u.x, o);
+        q8_word_int(u.y, o + 2);
         return make_h8(o[0], o[1], o[2], o[3]);
     } else {
         uint32_t o[4];
-        q4_word_int(k.w[b], o);
+        q4_word_int(*reinterpret_cast<const uint32_t*>(p), o);
         return make_h8(o[0], o[1], o[2], o[3]);
     }
+}
+
+// V of chunk row `key`, dims 16 c .. 16 c + 15, with its block scale
+template <int KVT>
+__device__ __forceinline__ void v_raw(VRaw<KVT>& r, const uint8_t* vst, const uint16_t* vsc, int key, int c) {
+    constexpr int VB = ChunkLds<KVT>::VB;
+    const uint8_t* p = vst + rot_off<KVT>(key, (VB / 16) * c);
+    if constexpr (KVT == QWA_KV_Q4_0) {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
+        r.w[0] = u.x; r.w[1] = u.y;
+    } else if constexpr (KVT == QWA_KV_Q8_0) {
+        const uint4 u = *reinterpret_cast<const uint4*>(p);
+        r.w[0] = u.x; r.w[1] = u.y; r.w[2] = u.z; r.w[3] = u.w;
+    } else {
+        const uint4 u0 = *reinterpret_cast<const uint4*>(p);
+        const uint4 u1 = *reinterpret_cast<const uint4*>(vst + rot_off<KVT>(key, 32 * c + 16));
+        r.w[0] = u0.x; r.w[1] = u0.y; r.w[2] = u0.z; r.w[3] = u0.w;
+        r.w[4] = u1.x; r.w[5] = u1.y; r.w[6] = u1.z; r.w[7] = u1.w;
+    }
+    r.sc = KVT == QWA_KV_F16 ? 0u : vsc[key * 8 + (c >> 1)];
 }
 
 __device__ __forceinline__ f4 mfma16k16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
-// One wave = one 256-key split x one 16-row tile.  Workgroup = SPW splits x RT row tiles (waves of the same split
-// share the K/V lines through L1 / L2).  NBUF chunks are in flight per wave (register ring).
-//
-// Scores are exact up to fp32 accumulation: K enters the MFMA as the exact integer codes and its fp16 block scale is
-// applied to each block's fp32 partial dot (one MFMA per 32-dim block); Q / 16 is split into fp16 hi + lo parts
-// (two MFMAs), i.e. ~22 significant bits.  This keeps large (outlier) logits within tolerance where fp16(Q) and
-// fp16(d * x) would not.
-template <int KVT, int RT, int SPW, int NBUF>
-__global__ void __launch_bounds__(64 * RT * SPW) __attribute__((amdgpu_waves_per_eu(2, 2)))
-k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int nsplit, float* __restrict__ work) {
-    // Q / 16 hi and lo parts in A-operand order: [rt][block][hi, lo][lane] x 8 halves (16 KB per row tile)
-    __shared__ h8 s_q[RT][8][2][64];
-    __shared__ float s_t[RT * SPW][16][20];  // per-wave transpose of the 16 x 16 score tile
+// Merge of two partial softmax states (fold step); the same arithmetic for every record and every nq.
+__device__ __forceinline__ void fold(float& m, float& l, f4* o, float m2, float l2, const f4* o2) {
+    const float M = fmaxf(m, m2);
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    const float fa = fast_exp2((m - Ms) * LOG2E), fb = fast_exp2((m2 - Ms) * LOG2E);
+    l = l * fa + l2 * fb;
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++) o[dt] = o[dt] * fa + o2[dt] * fb;
+    m = M;
+}
+
+// ring depth (chunks in flight per wave): sized so that two 4-wave workgroups fit a CU's 160 KB of LDS where possible
+template <int KVT, int RT> struct DecCfg {
+    static constexpr int NST = KVT == QWA_KV_Q4_0 ? (RT == 1 ? 3 : 2) : 1;
+};
+
+// RT row tiles starting at tile rt0 (calls with more tiles launch several passes; a row's arithmetic is the same
+// in every pass and every grouping).
+template <int KVT, int RT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work) {
+    using C = ChunkLds<KVT>;
+    constexpr int NST = DecCfg<KVT, RT>::NST;
+    // the chunk ring of every wave while streaming; two partial states while merging
+    __shared__ __attribute__((aligned(16))) union {
+        uint8_t ring[WG_CLASSES][NST][C::BYTES];
+        struct {
+            f4 o[2][16][64];
+            float ml[2][2][64];
+        } merge;
+    } s_u;
+    __shared__ h8 s_q[RT][8][2][64];  // Q / 16 hi and lo parts in B-operand order [tile][block][hi, lo][lane]
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
-    const int g = blockIdx.y;
+    const int g = blockIdx.y, rec = blockIdx.x;
     const int kmax = pos0 + nq - 1;
+    const int nchunk = kmax / CHUNK + 1;
+    const int cls = rec * WG_CLASSES + wave;
+    const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;  // chunks of this wave
+    const size_t rowbase = (size_t)g * kv.capacity;
 
-    for (int e = threadIdx.x; e < RT * 8 * 64; e += 64 * RT * SPW) {
+    for (int e = threadIdx.x; e < RT * 8 * 64; e += 256) {
         const int rt = e >> 9, b = (e >> 6) & 7, ln = e & 63;
-        const int r = 16 * rt + (ln & 15);
+        const int r = 16 * (rt0 + rt) + (ln & 15);
         const int qt = r / GRP, hh = r % GRP;
         h8 hi, lo;
         if (qt < nq) {
@@ -148,125 +199,185 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int nsplit
     }
     __syncthreads();
 
-    const int split = blockIdx.x * SPW + wave / RT;
-    const int rt = wave % RT;
-    if (split >= nsplit) return;
-    // this lane's row in the S^T layout: query qt, head hh, last visible key qpos (-1: padding row)
-    const int r = 16 * rt + i16;
-    const int qt = r / GRP, hh = r % GRP;
-    const int qpos = qt < nq ? pos0 + qt : -1;
-    float (*tr)[20] = s_t[wave];
+    // rows of this lane (S^T layout, column i16): query qt, head hh, last visible key qpos (-1: padding row)
+    int qpos[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int r = 16 * (rt0 + rt) + i16;
+        qpos[rt] = r / GRP < nq ? pos0 + r / GRP : -1;
+    }
+    f4 o[RT][16];
+    float m[RT], l[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        m[rt] = -INFINITY;
+        l[rt] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) o[rt][dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 
-    f4 o[16];
+    if (nmine > 0) {
+        const int klim = kmax;
+        uint8_t(*ring)[C::BYTES] = s_u.ring[wave];
+        auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * min(j, nmine - 1)); };
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m = -INFINITY, l = 0.0f;
+        for (int s = 0; s < NST; s++) issue_chunk<KVT>(ring[s], kv, rowbase, chunk_key(s), klim, lane);
+        for (int j = 0; j < nmine; j++) {
+            const int slot = j % NST;
+            const int kb = chunk_key(j);
+            wait_vmcnt<C::NLOAD * (NST - 1)>();  // this slot has landed; the later ones may still fly
+            __builtin_amdgcn_wave_barrier();
+            const uint8_t* kst = ring[slot];
+            const uint8_t* vst = kst + C::KBYTES;
+            const uint16_t* ksc = reinterpret_cast<const uint16_t*>(kst + 2 * C::KBYTES);
+            const uint16_t* vsc = reinterpret_cast<const uint16_t*>(kst + 2 * C::KBYTES + C::SC);
 
-    const int k_begin = split * DEC_SPLIT;
-    const int k_end = min(k_begin + DEC_SPLIT, kmax + 1);
-    const size_t rowbase = (size_t)g * kv.capacity;
-    Chunk<KVT> buf[NBUF];
+            // ---- S^T = K Q^T (16 keys x 16 rows per tile): per block K_int . (Q_hi + Q_lo), times the key's scale
+            uint32_t kd[4][4];  // block scales of this lane's 4 keys 4 lg + i
+            if constexpr (KVT != QWA_KV_F16) {
 #pragma unroll
-    for (int b = 0; b < NBUF; b++)
-        if (k_begin + 16 * b < k_end) load_chunk<KVT>(buf[b], kv, rowbase, k_begin + 16 * b, kmax, i16, lg);
-
-    for (int kb0 = k_begin; kb0 < k_end; kb0 += 16 * NBUF) {
-#pragma unroll
-        for (int bi = 0; bi < NBUF; bi++) {
-            const int kb = kb0 + 16 * bi;
-            if (kb >= k_end) break;
-            const Chunk<KVT>& c = buf[bi];
-
-            // ---- S = Q K^T (16 rows x 16 keys): per block, (Q_hi + Q_lo) . K_int, scaled by the key's block scale
-            f4 S = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int b = 0; b < 8; b++) {
-                const h8 kb8 = k_block_int<KVT>(c.k, b);
-                f4 a = mfma16(s_q[rt][b][0][lane], kb8, f4{0.0f, 0.0f, 0.0f, 0.0f});
-                a = mfma16(s_q[rt][b][1][lane], kb8, a);
-                if constexpr (KVT == QWA_KV_F16) {
-                    S += a;
-                } else {
-                    const float d = h2f_bits((uint16_t)(c.k.sc[b >> 1] >> (16 * (b & 1))));
-#pragma unroll
-                    for (int i = 0; i < 4; i++) S[i] = fmaf(d, a[i], S[i]);
+                for (int i = 0; i < 4; i++) {
+                    const uint4 u = *reinterpret_cast<const uint4*>(ksc + (4 * lg + i) * 8);
+                    kd[i][0] = u.x; kd[i][1] = u.y; kd[i][2] = u.z; kd[i][3] = u.w;
                 }
             }
-            // lane (key i16, g) holds rows 4 g + i -> transpose through LDS to lane (row i16, g) holding keys 4 g + i
+            f4 S[RT];
 #pragma unroll
-            for (int i = 0; i < 4; i++) tr[4 * lg + i][i16] = S[i];
-            __builtin_amdgcn_wave_barrier();
-            const float4 st = *reinterpret_cast<const float4*>(&tr[i16][4 * lg]);
-            __builtin_amdgcn_wave_barrier();
+            for (int rt = 0; rt < RT; rt++) S[rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const h8 ka = k_block_int<KVT>(kst, i16, lg, b);
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++) {
+                    f4 a = mfma16(ka, s_q[rt][b][0][lane], f4{0.0f, 0.0f, 0.0f, 0.0f});
+                    a = mfma16(ka, s_q[rt][b][1][lane], a);
+                    if constexpr (KVT == QWA_KV_F16) {
+                        S[rt] += a;
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const float d = h2f_bits((uint16_t)(kd[i][b >> 1] >> (16 * (b & 1))));
+                            S[rt][i] = fmaf(d, a[i], S[rt][i]);
+                        }
+                    }
+                }
+            }
 
             // ---- causal mask + online softmax: lane holds keys kb + 4 lg + i of its row
-            const float sc4[4] = {st.x, st.y, st.z, st.w};
-            float sv[4];
-            float mx = -INFINITY;
+            h4 p[RT];
+            float cr[RT];
+            bool moved = false;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                sv[i] = kb + 4 * lg + i <= qpos ? sc4[i] : -INFINITY;
-                mx = fmaxf(mx, sv[i]);
+            for (int rt = 0; rt < RT; rt++) {
+                float sv[4];
+                float mx = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    sv[i] = kb + 4 * lg + i <= qpos[rt] ? S[rt][i] : -INFINITY;
+                    mx = fmaxf(mx, sv[i]);
+                }
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float mn = fmaxf(m[rt], mx);
+                const float msl = (mn == -INFINITY ? 0.0f : mn) * LOG2E;  // a row that saw nothing keeps l = 0, O = 0
+                cr[rt] = fast_exp2(m[rt] * LOG2E - msl);
+                float rs = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float e = fast_exp2(fmaf(sv[i], LOG2E, -msl));
+                    rs += e;
+                    p[rt][i] = (_Float16)e;
+                }
+                l[rt] = l[rt] * cr[rt] + rs;
+                m[rt] = mn;
+                moved |= cr[rt] != 1.0f;
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = fmaxf(m, mx);
-            const float msl = (mn == -INFINITY ? 0.0f : mn) * LOG2E;  // a row that saw nothing keeps l = 0, O = 0
-            const float cr = fast_exp2(m * LOG2E - msl);
-            h4 p;
-            float rs = 0.0f;
+            if (__any(moved)) {  // multiplying by exactly 1 is the identity
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float e = fast_exp2(fmaf(sv[i], LOG2E, -msl));
-                rs += e;
-                p[i] = (_Float16)e;
-            }
-            l = l * cr + rs;
-            m = mn;
-            // rescale only when some row's max moved (multiplying by exactly 1 is the identity)
-            if (__any(cr != 1.0f)) {
+                for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-                for (int dt = 0; dt < 16; dt++) o[dt] *= cr;
+                    for (int dt = 0; dt < 16; dt++) o[rt][dt] *= cr[rt];
             }
 
             // ---- O^T += V^T P^T: 16 dim tiles (lane dim 16 i16 + dt), keys 4 lg .. 4 lg + 3
-            constexpr int NW = sizeof(c.v[0].w) / 4;  // raw words per 16 dims
-            constexpr int DPW = 16 / NW;              // dims per raw word
+            VRaw<KVT> vr[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) v_raw<KVT>(vr[jj], vst, vsc, 4 * lg + jj, i16);
+            __builtin_amdgcn_wave_barrier();
+            // the slot is consumed: refill it with the chunk NST ahead (clamped: re-reads cached lines at the end)
+            issue_chunk<KVT>(ring[slot], kv, rowbase, chunk_key(j + NST), klim, lane);
+            constexpr int NW = sizeof(vr[0].w) / 4;  // raw words per 16 dims
+            constexpr int DPW = 16 / NW;             // dims per raw word
 #pragma unroll
             for (int wi = 0; wi < NW; wi++) {
                 uint32_t w01[DPW], w23[DPW];
-                v_pair_words<KVT, 1>(&c.v[0].w[wi], &c.v[1].w[wi], c.v[0].sc, c.v[1].sc, w01);
-                v_pair_words<KVT, 1>(&c.v[2].w[wi], &c.v[3].w[wi], c.v[2].sc, c.v[3].sc, w23);
+                v_pair_words<KVT, 1>(&vr[0].w[wi], &vr[1].w[wi], vr[0].sc, vr[1].sc, w01);
+                v_pair_words<KVT, 1>(&vr[2].w[wi], &vr[3].w[wi], vr[2].sc, vr[3].sc, w23);
 #pragma unroll
                 for (int d = 0; d < DPW; d++) {
-                    const int dt = wi * DPW + d;
-                    o[dt] = mfma16k16(make_h4(w01[d], w23[d]), p, o[dt]);
+                    const h4 a = make_h4(w01[d], w23[d]);
+#pragma unroll
+                    for (int rt = 0; rt < RT; rt++) o[rt][wi * DPW + d] = mfma16k16(a, p[rt], o[rt][wi * DPW + d]);
                 }
             }
-
-            // ---- refill this slot with the chunk NBUF ahead
-            const int kn = kb + 16 * NBUF;
-            if (kn < k_end) load_chunk<KVT>(buf[bi], kv, rowbase, kn, kmax, i16, lg);
         }
+        wait_vmcnt<0>();  // drain the clamped prefetches before the ring is reused or the wave exits
     }
 
-    // ---- partial record of the row: m, l (summed over the 4 lanes of the row), O at dims 64 lg + 16 i + dt
-    float lt = l;
-    lt += __shfl_xor(lt, 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
-    if (qpos < 0) return;
-    float* rec = work + ((((size_t)split * NKV + g) * MAXQ + qt) * GRP + hh) * REC;
-    if (lg == 0) {
-        rec[0] = m;
-        rec[1] = lt;
-    }
+    // ---- merge the 4 classes as fold(fold(c0, c1), fold(c2, c3)) per row tile; wave 0 writes the records
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float* dst = rec + 4 + 64 * lg + 16 * i;
+    for (int rt = 0; rt < RT; rt++) {
+        __syncthreads();  // every wave is done with the ring (or with the previous tile's merge)
+        if (wave & 1) {
 #pragma unroll
-        for (int d4 = 0; d4 < 4; d4++)
-            *reinterpret_cast<float4*>(dst + 4 * d4) =
-                make_float4(o[4 * d4][i], o[4 * d4 + 1][i], o[4 * d4 + 2][i], o[4 * d4 + 3][i]);
+            for (int dt = 0; dt < 16; dt++) s_u.merge.o[wave >> 1][dt][lane] = o[rt][dt];
+            s_u.merge.ml[wave >> 1][0][lane] = m[rt];
+            s_u.merge.ml[wave >> 1][1][lane] = l[rt];
+        }
+        __syncthreads();
+        if (!(wave & 1)) {
+            f4 o2[16];
+#pragma unroll
+            for (int dt = 0; dt < 16; dt++) o2[dt] = s_u.merge.o[wave >> 1][dt][lane];
+            fold(m[rt], l[rt], o[rt], s_u.merge.ml[wave >> 1][0][lane], s_u.merge.ml[wave >> 1][1][lane], o2);
+        }
+        __syncthreads();
+        if (wave == 2) {
+#pragma unroll
+            for (int dt = 0; dt < 16; dt++) s_u.merge.o[0][dt][lane] = o[rt][dt];
+            s_u.merge.ml[0][0][lane] = m[rt];
+            s_u.merge.ml[0][1][lane] = l[rt];
+        }
+        __syncthreads();
+        if (wave == 0) {
+            {
+                f4 o2[16];
+#pragma unroll
+                for (int dt = 0; dt < 16; dt++) o2[dt] = s_u.merge.o[0][dt][lane];
+                fold(m[rt], l[rt], o[rt], s_u.merge.ml[0][0][lane], s_u.merge.ml[0][1][lane], o2);
+            }
+            float lt = l[rt];
+            lt += __shfl_xor(lt, 16, 64);
+            lt += __shfl_xor(lt, 32, 64);
+            const int r = 16 * (rt0 + rt) + i16;
+            const int qt = r / GRP, hh = r % GRP;
+            if (qpos[rt] >= 0) {
+                float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt) * GRP + hh) * REC;
+                if (lg == 0) {
+                    recp[0] = m[rt];
+                    recp[1] = lt;
+                }
+                // O^T C layout: lane (row i16, g) holds dims 16 (4 g + i) + dt
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    float* dst = recp + 4 + 64 * lg + 16 * i;
+#pragma unroll
+                    for (int d4 = 0; d4 < 4; d4++)
+                        *reinterpret_cast<float4*>(dst + 4 * d4) = make_float4(
+                            o[rt][4 * d4][i], o[rt][4 * d4 + 1][i], o[rt][4 * d4 + 2][i], o[rt][4 * d4 + 3][i]);
+                }
+            }
+        }
     }
 }
 
@@ -277,7 +388,7 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int nsplit
 __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ work, int nsplit,
                                                      const float* __restrict__ gate, float* __restrict__ out,
                                                      float* __restrict__ out_host, qwa_act_q8 oq, int do_q) {
-    constexpr int MAXSPLIT = MAX_POS / DEC_SPLIT + 1;
+    constexpr int MAXSPLIT = NREC;
     constexpr int MAXGRP = (MAXSPLIT + CGRP - 1) / CGRP;
     __shared__ float s_f[MAXSPLIT];
     __shared__ float s_l[MAXSPLIT];
@@ -352,25 +463,18 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
 }
 
 template <int KVT>
-static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int nq, int nsplit, float* work,
+static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int nq, int nrec, float* work,
                            hipStream_t st) {
     const int rt = (GRP * nq + 15) / 16;
-    constexpr int NB = KVT == QWA_KV_Q4_0 ? 4 : KVT == QWA_KV_Q8_0 ? 2 : 1;
-    if (rt == 1) {
-        hipLaunchKernelGGL((k_dec<KVT, 1, 4, NB>), dim3((nsplit + 3) / 4, NKV), dim3(256), 0, st, q, kv, pos0, nq,
-                           nsplit, work);
-    } else if (rt == 2) {
-        hipLaunchKernelGGL((k_dec<KVT, 2, 2, NB>), dim3((nsplit + 1) / 2, NKV), dim3(256), 0, st, q, kv, pos0, nq,
-                           nsplit, work);
-    } else {
-        hipLaunchKernelGGL((k_dec<KVT, 3, 2, NB>), dim3((nsplit + 1) / 2, NKV), dim3(384), 0, st, q, kv, pos0, nq,
-                           nsplit, work);
-    }
+    const dim3 grid(nrec, NKV);
+    for (int t = 0; t < rt; t++) hipLaunchKernelGGL((k_dec<KVT, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
 }
 
 hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int pos0, int nq,
                          void* work, float* out, const qwa_act_q8* oq, float* out_host, hipStream_t st) {
-    const int nsplit = dec_nsplit(pos0 + nq - 1);
+    // one record per workgroup; workgroups past the last chunk would hold no class with a chunk
+    const int nchunk = (pos0 + nq - 1) / CHUNK + 1;
+    const int nsplit = min(NREC, (nchunk + WG_CLASSES - 1) / WG_CLASSES);
     float* w = static_cast<float*>(work);
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, w, st);
     else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, w, st);

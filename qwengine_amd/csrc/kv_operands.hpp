@@ -95,10 +95,15 @@ __device__ __forceinline__ h8 k_operand(const KRaw<KVT>& r, int s) {
 
 // Exact small integers as fp16 (no scale): the codes c - 8 of a Q4_0 word in the k_operand order, or the int8
 // values of a Q8_0 word.
+// (the low nibbles of the 4 bytes go to bytes {0, 2} / {1, 3} of two perm results: {e0,e4}, {e2,e6}; the high
+// nibbles likewise give {e1,e5}, {e3,e7})
 __device__ __forceinline__ void q4_word_int(uint32_t w, uint32_t* out) {
     const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
-#pragma unroll
-    for (int k = 0; k < 4; k++) out[k] = h2_bits(bits_h2(((w >> (4 * k)) & 0x000F000Fu) | 0x64006400u) - bias);
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    out[0] = h2_bits(bits_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04020400u)) - bias);  // e0, e4
+    out[1] = h2_bits(bits_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04020400u)) - bias);  // e1, e5
+    out[2] = h2_bits(bits_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030401u)) - bias);  // e2, e6
+    out[3] = h2_bits(bits_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030401u)) - bias);  // e3, e7
 }
 __device__ __forceinline__ void q8_word_int(uint32_t w, uint32_t* out) {
     const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};

@@ -18,9 +18,8 @@ hipError_t launch_rope_table_pos(const int* pos3, int B, float theta, float* rop
 hipError_t launch_kv_append(const float* xk, const float* xv, int pos0, int n, int kvt, const qwa_kv_layer& kv,
                             hipStream_t st);
 
-// split-K decode: number of fixed 256-key splits covering keys [0, kmax]
-constexpr int DEC_SPLIT = 256;
-inline int dec_nsplit(int kmax) { return kmax / DEC_SPLIT + 1; }
+// split-K decode: 16-key chunks in DEC_CLASSES fixed residue classes per KV head (chunk index mod DEC_CLASSES)
+constexpr int DEC_CLASSES = 512;
 size_t dec_work_bytes(int n_pos);
 hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int pos0, int nq,
                          void* work, float* out, const qwa_act_q8* oq, float* out_host, hipStream_t st);
