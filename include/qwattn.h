@@ -121,6 +121,14 @@ int qwa_attn_prefill_simple(const float* q, const float* gate, const qwa_kv_laye
  * (src/cuda/common.cuh:199-228), exposed on its own so callers holding already-roped K can append them. */
 int qwa_kv_append(const float* xk, const float* xv, int pos0, int n, int kvt, const qwa_kv_layer* kv, void* stream);
 
+/* Opt-in kernel timing (no reference counterpart; the reference times phases with env-gated GPU timers,
+ * src/runtime/engine.cpp:2477-2480): between qwa_profile_begin() and qwa_profile_end(), every attention call records
+ * HIP events around its main kernel (decode: the split-K kernel; prefill: the MFMA kernel).  qwa_profile_end()
+ * synchronizes those events and returns the summed kernel time in ms and the number of timed launches.  At most
+ * 65536 launches per window; events are created on first use and kept by the library. */
+int qwa_profile_begin(void);
+int qwa_profile_end(double* total_ms, int* launches);
+
 /* Human-readable text of a status code, and of the last error recorded by this library in the calling thread. */
 const char* qwa_status_string(int status);
 const char* qwa_last_error(void);

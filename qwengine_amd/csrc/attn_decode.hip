@@ -33,54 +33,56 @@ constexpr int CHUNK = 16;   // keys per chunk
 constexpr int WG_CLASSES = 4;
 constexpr int NREC = DEC_CLASSES / WG_CLASSES;  // records (workgroups) per KV head
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr float RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maximum (natural-log units)
 
 size_t dec_work_bytes(int n_pos) {
     (void)n_pos;
     return (size_t)NREC * NKV * MAXQ * GRP * REC * sizeof(float);
 }
 
-// one 16-key chunk in LDS: K rows, V rows (VB bytes each, 16-byte pieces rotated by the row index), block scales
+// One 16-key chunk in LDS.  K: piece-major, 16-byte piece p of row n at (16 p + n) * 16 (an MFMA operand read of one
+// quant block is then a conflict-free read at a fixed offset); V: row-major; then the K and V block scales
+// ([row][8] fp16 each).
 template <int KVT>
 struct ChunkLds {
     static constexpr int VB = value_bytes(KVT);
-    static constexpr int PIECES = VB / 16;  // 16-byte pieces per row
     static constexpr int KBYTES = CHUNK * VB;
+    static constexpr int NI = KBYTES / 1024;  // 1 KB load instructions per K (and per V) region
     static constexpr int SC = KVT == QWA_KV_F16 ? 0 : CHUNK * 16;
     static constexpr int BYTES = 2 * KBYTES + 2 * SC;
-    static constexpr int NLOAD = 2 * KBYTES / 1024 + (SC ? 2 : 0);  // load instructions per chunk
+    static constexpr int NLOAD = 2 * NI + (SC ? 2 : 0);  // load instructions per chunk
 };
 
-// LDS offset of byte `byte` (< VB) of row `row` (pieces rotated by row)
+// LDS offset of byte `byte` (< VB) of K row `row` in the piece-major layout
 template <int KVT>
-__device__ __forceinline__ int rot_off(int row, int byte) {
-    constexpr int VB = ChunkLds<KVT>::VB, P = ChunkLds<KVT>::PIECES;
-    return row * VB + 16 * (((byte >> 4) + row) % P) + (byte & 15);
+__host__ __device__ constexpr int kpos(int row, int byte) {
+    return ((byte >> 4) * CHUNK + row) * 16 + (byte & 15);
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Issue the direct-to-LDS loads of chunk `kb` (rows past klim re-read row klim: no branch, no read outside the
-// window; their scores are masked and their probabilities are exact zeros).
+// Direct-to-LDS loads of one chunk (16 B per lane per instruction: K piece-major, V row-major, then the scales).
+// Rows past kmax re-read row kmax (no read outside the window; their scores are masked and their probabilities are
+// exact zeros).
 template <int KVT>
-__device__ __forceinline__ void issue_chunk(uint8_t* dst, const qwa_kv_layer& kv, size_t rowbase, int kb, int klim,
-                                            int lane) {
+__device__ __forceinline__ void issue_chunk(uint8_t* dst, const qwa_kv_layer& kv, size_t rowbase, int kb, int kmax,
+                                           int lane) {
     using C = ChunkLds<KVT>;
-    constexpr int VB = C::VB, P = C::PIECES;
+    constexpr int VB = C::VB;
 #pragma unroll
-    for (int i = 0; i < C::KBYTES / 1024; i++) {
-        // LDS slot (row, s) <- global piece (s - row) mod P of that row
-        const int slot = lane + 64 * i, row = slot / P, s = slot % P;
-        const int piece = (s - row % P + P) % P;
-        const size_t grow = rowbase + min(kb + row, klim);
-        __builtin_amdgcn_global_load_lds(kv.k + grow * VB + 16 * piece, (lds_void*)(dst + 1024 * i), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(kv.v + grow * VB + 16 * piece, (lds_void*)(dst + C::KBYTES + 1024 * i), 16,
-                                         0, 0);
+    for (int i = 0; i < C::NI; i++) {
+        const int kn = lane & 15, kp = 4 * i + (lane >> 4);                 // K slot: piece kp of row kn
+        const int vn = (1024 * i + 16 * lane) / VB, vbyte = (1024 * i + 16 * lane) % VB;  // V: row-major
+        __builtin_amdgcn_global_load_lds(kv.k + (rowbase + min(kb + kn, kmax)) * VB + 16 * kp,
+                                         (lds_void*)(dst + 1024 * i), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(kv.v + (rowbase + min(kb + vn, kmax)) * VB + vbyte,
+                                         (lds_void*)(dst + C::KBYTES + 1024 * i), 16, 0, 0);
     }
     if constexpr (C::SC) {
-        const size_t grow = rowbase + min(kb + lane / 4, klim);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(kv.ks + grow * 8) + 4 * (lane & 3),
+        const size_t row = rowbase + min(kb + lane / 4, kmax);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(kv.ks + row * 8) + 4 * (lane & 3),
                                          (lds_void*)(dst + 2 * C::KBYTES), 4, 0, 0);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(kv.vs + grow * 8) + 4 * (lane & 3),
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(kv.vs + row * 8) + 4 * (lane & 3),
                                          (lds_void*)(dst + 2 * C::KBYTES + C::SC), 4, 0, 0);
     }
 }
@@ -95,7 +97,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <int KVT>
 __device__ __forceinline__ h8 k_block_int(const uint8_t* kst, int n, int g, int b) {
     constexpr int VB = ChunkLds<KVT>::VB;
-    const uint8_t* p = kst + rot_off<KVT>(n, (VB / 8) * b + (VB / 32) * g);
+    const uint8_t* p = kst + kpos<KVT>(n, (VB / 8) * b + (VB / 32) * g);
     if constexpr (KVT == QWA_KV_F16) {
         return *reinterpret_cast<const h8*>(p);
     } else if constexpr (KVT == QWA_KV_Q8_0) {
@@ -115,7 +117,7 @@ __device__ __forceinline__ h8 k_block_int(const uint8_t* kst, int n, int g, int 
 template <int KVT>
 __device__ __forceinline__ void v_raw(VRaw<KVT>& r, const uint8_t* vst, const uint16_t* vsc, int key, int c) {
     constexpr int VB = ChunkLds<KVT>::VB;
-    const uint8_t* p = vst + rot_off<KVT>(key, (VB / 16) * c);
+    const uint8_t* p = vst + key * VB + (VB / 16) * c;
     if constexpr (KVT == QWA_KV_Q4_0) {
         const uint2 u = *reinterpret_cast<const uint2*>(p);
         r.w[0] = u.x; r.w[1] = u.y;
@@ -123,12 +125,19 @@ __device__ __forceinline__ void v_raw(VRaw<KVT>& r, const uint8_t* vst, const ui
         const uint4 u = *reinterpret_cast<const uint4*>(p);
         r.w[0] = u.x; r.w[1] = u.y; r.w[2] = u.z; r.w[3] = u.w;
     } else {
-        const uint4 u0 = *reinterpret_cast<const uint4*>(p);
-        const uint4 u1 = *reinterpret_cast<const uint4*>(vst + rot_off<KVT>(key, 32 * c + 16));
+        const uint4 u0 = *reinterpret_cast<const uint4*>(p), u1 = *reinterpret_cast<const uint4*>(p + 16);
         r.w[0] = u0.x; r.w[1] = u0.y; r.w[2] = u0.z; r.w[3] = u0.w;
         r.w[4] = u1.x; r.w[5] = u1.y; r.w[6] = u1.z; r.w[7] = u1.w;
     }
     r.sc = KVT == QWA_KV_F16 ? 0u : vsc[key * 8 + (c >> 1)];
+}
+
+// max over the 4 lanes l % 16 + 16 k (the 4 lanes that hold one row of S^T): two cross-row swaps, no LDS
+__device__ __forceinline__ float row_max4(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ f4 mfma16k16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
@@ -164,7 +173,6 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
             float ml[2][2][64];
         } merge;
     } s_u;
-    __shared__ h8 s_q[RT][8][2][64];  // Q / 16 hi and lo parts in B-operand order [tile][block][hi, lo][lane]
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
     const int g = blockIdx.y, rec = blockIdx.x;
@@ -174,30 +182,27 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;  // chunks of this wave
     const size_t rowbase = (size_t)g * kv.capacity;
 
-    for (int e = threadIdx.x; e < RT * 8 * 64; e += 256) {
-        const int rt = e >> 9, b = (e >> 6) & 7, ln = e & 63;
-        const int r = 16 * (rt0 + rt) + (ln & 15);
+    // Q / 16 as fp16 hi + lo parts, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + perm(j)
+    h8 qh[RT][8], ql[RT][8];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int r = 16 * (rt0 + rt) + i16;
         const int qt = r / GRP, hh = r % GRP;
-        h8 hi, lo;
-        if (qt < nq) {
-            const float* src = q + ((size_t)qt * NH + g * GRP + hh) * HD + 32 * b + 8 * (ln >> 4);
-            const float4 a = *reinterpret_cast<const float4*>(src);
-            const float4 c = *reinterpret_cast<const float4*>(src + 4);
+        const bool valid = qt < nq;
+        const float* src = q + ((size_t)(valid ? qt : 0) * NH + g * GRP + hh) * HD + 8 * lg;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const float4 a = *reinterpret_cast<const float4*>(src + 32 * b);
+            const float4 c = *reinterpret_cast<const float4*>(src + 32 * b + 4);
             const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const float v = x[k_perm<KVT>(j)] * 0.0625f;
-                hi[j] = (_Float16)v;
-                lo[j] = (_Float16)(v - (float)hi[j]);
+                const float v = valid ? x[k_perm<KVT>(j)] * 0.0625f : 0.0f;
+                qh[rt][b][j] = (_Float16)v;
+                ql[rt][b][j] = (_Float16)(v - (float)qh[rt][b][j]);
             }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) hi[j] = lo[j] = (_Float16)0.0f;
         }
-        s_q[rt][b][0][ln] = hi;
-        s_q[rt][b][1][ln] = lo;
     }
-    __syncthreads();
 
     // rows of this lane (S^T layout, column i16): query qt, head hh, last visible key qpos (-1: padding row)
     int qpos[RT];
@@ -217,11 +222,11 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     }
 
     if (nmine > 0) {
-        const int klim = kmax;
         uint8_t(*ring)[C::BYTES] = s_u.ring[wave];
         auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * min(j, nmine - 1)); };
+        auto issue = [&](uint8_t* dst, int kb) { issue_chunk<KVT>(dst, kv, rowbase, kb, kmax, lane); };
 #pragma unroll
-        for (int s = 0; s < NST; s++) issue_chunk<KVT>(ring[s], kv, rowbase, chunk_key(s), klim, lane);
+        for (int st = 0; st < NST; st++) issue(ring[st], chunk_key(st));
         for (int j = 0; j < nmine; j++) {
             const int slot = j % NST;
             const int kb = chunk_key(j);
@@ -249,8 +254,8 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
                 const h8 ka = k_block_int<KVT>(kst, i16, lg, b);
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
-                    f4 a = mfma16(ka, s_q[rt][b][0][lane], f4{0.0f, 0.0f, 0.0f, 0.0f});
-                    a = mfma16(ka, s_q[rt][b][1][lane], a);
+                    f4 a = mfma16(ka, qh[rt][b], f4{0.0f, 0.0f, 0.0f, 0.0f});
+                    a = mfma16(ka, ql[rt][b], a);
                     if constexpr (KVT == QWA_KV_F16) {
                         S[rt] += a;
                     } else {
@@ -263,24 +268,26 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
                 }
             }
 
-            // ---- causal mask + online softmax: lane holds keys kb + 4 lg + i of its row
+            // ---- online softmax, lane holding keys kb + 4 lg + i of its row.  Causal masking only in chunks that
+            // reach past the first query's position.  The reference maximum m moves only when a score exceeds it by
+            // more than RESCALE_T (probabilities stay <= e^RESCALE_T, far inside fp16), so O is rarely rescaled.
+            const bool tail = kb + CHUNK - 1 > pos0;
             h4 p[RT];
             float cr[RT];
             bool moved = false;
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
                 float sv[4];
-                float mx = -INFINITY;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    sv[i] = kb + 4 * lg + i <= qpos[rt] ? S[rt][i] : -INFINITY;
-                    mx = fmaxf(mx, sv[i]);
+                for (int i = 0; i < 4; i++) sv[i] = S[rt][i];
+                if (tail) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sv[i] = kb + 4 * lg + i <= qpos[rt] ? sv[i] : -INFINITY;
                 }
-                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                const float mn = fmaxf(m[rt], mx);
+                const float mx = row_max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+                const float mn = mx > m[rt] + RESCALE_T ? mx : m[rt];
                 const float msl = (mn == -INFINITY ? 0.0f : mn) * LOG2E;  // a row that saw nothing keeps l = 0, O = 0
-                cr[rt] = fast_exp2(m[rt] * LOG2E - msl);
+                cr[rt] = mn == m[rt] ? 1.0f : fast_exp2(m[rt] * LOG2E - msl);
                 float rs = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -305,7 +312,7 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
             for (int jj = 0; jj < 4; jj++) v_raw<KVT>(vr[jj], vst, vsc, 4 * lg + jj, i16);
             __builtin_amdgcn_wave_barrier();
             // the slot is consumed: refill it with the chunk NST ahead (clamped: re-reads cached lines at the end)
-            issue_chunk<KVT>(ring[slot], kv, rowbase, chunk_key(j + NST), klim, lane);
+            issue(ring[slot], chunk_key(j + NST));
             constexpr int NW = sizeof(vr[0].w) / 4;  // raw words per 16 dims
             constexpr int DPW = 16 / NW;             // dims per raw word
 #pragma unroll
@@ -476,9 +483,11 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     const int nchunk = (pos0 + nq - 1) / CHUNK + 1;
     const int nsplit = min(NREC, (nchunk + WG_CLASSES - 1) / WG_CLASSES);
     float* w = static_cast<float*>(work);
+    profile_mark_begin(st);
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, w, st);
     else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, w, st);
     else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, w, st);
+    profile_mark_end(st);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const qwa_act_q8 a = oq ? *oq : qwa_act_q8{nullptr, nullptr, nullptr};

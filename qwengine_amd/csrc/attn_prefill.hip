@@ -288,9 +288,11 @@ k_prefill(const float* __restrict__ q, const float* __restrict__ gate, qwa_kv_la
 hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
                           uint16_t* out16, hipStream_t st) {
     const dim3 grid((GRP * B + PF_ROWS - 1) / PF_ROWS, NKV);
+    profile_mark_begin(st);
     if (kvt == QWA_KV_F16) hipLaunchKernelGGL(k_prefill<QWA_KV_F16>, grid, dim3(256), 0, st, q, gate, kv, B, p0, out16);
     else if (kvt == QWA_KV_Q8_0) hipLaunchKernelGGL(k_prefill<QWA_KV_Q8_0>, grid, dim3(256), 0, st, q, gate, kv, B, p0, out16);
     else hipLaunchKernelGGL(k_prefill<QWA_KV_Q4_0>, grid, dim3(256), 0, st, q, gate, kv, B, p0, out16);
+    profile_mark_end(st);
     return hipGetLastError();
 }
 

@@ -2,6 +2,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <vector>
+
 #include "launch.hpp"
 #include "qwattn_common.hpp"
 
@@ -45,7 +47,37 @@ int check_src(const qwa_row_src* s, int n, const char* what, const char* fn) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+// kernel timing window
+constexpr int PROF_MAX = 65536;
+struct Profile {
+    bool on = false;
+    int n = 0;
+    std::vector<hipEvent_t> ev;  // 2 per launch, created lazily
+} g_prof;
+
 }  // namespace
+
+namespace qwa {
+
+static void prof_record(hipStream_t st, int which) {
+    if (!g_prof.on || g_prof.n >= PROF_MAX) return;
+    const size_t idx = 2 * (size_t)g_prof.n + which;
+    while (g_prof.ev.size() <= idx) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) {
+            g_prof.on = false;
+            return;
+        }
+        g_prof.ev.push_back(e);
+    }
+    hipEventRecord(g_prof.ev[idx], st);
+    if (which == 1) g_prof.n++;
+}
+
+void profile_mark_begin(hipStream_t st) { prof_record(st, 0); }
+void profile_mark_end(hipStream_t st) { prof_record(st, 1); }
+
+}  // namespace qwa
 
 extern "C" {
 
@@ -184,6 +216,29 @@ int qwa_kv_append(const float* xk, const float* xv, int pos0, int n, int kvt, co
         return fail(QWA_ERR_RANGE, "%s: positions [%d, %d) outside the cache capacity %d", fn, pos0, pos0 + n,
                     kv->capacity);
     return from_hip(qwa::launch_kv_append(xk, xv, pos0, n, kvt, *kv, as_stream(stream)), fn);
+}
+
+int qwa_profile_begin(void) {
+    g_prof.on = true;
+    g_prof.n = 0;
+    return QWA_OK;
+}
+
+int qwa_profile_end(double* total_ms, int* launches) {
+    g_prof.on = false;
+    double tot = 0.0;
+    for (int i = 0; i < g_prof.n; i++) {
+        hipError_t e = hipEventSynchronize(g_prof.ev[2 * i + 1]);
+        if (e != hipSuccess) return from_hip(e, "profile_end");
+        float ms = 0.0f;
+        e = hipEventElapsedTime(&ms, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]);
+        if (e != hipSuccess) return from_hip(e, "profile_end");
+        tot += ms;
+    }
+    if (total_ms) *total_ms = tot;
+    if (launches) *launches = g_prof.n;
+    g_prof.n = 0;
+    return QWA_OK;
 }
 
 const char* qwa_status_string(int status) {

@@ -7,6 +7,10 @@
 
 namespace qwa {
 
+// opt-in kernel timing (qwa_profile_begin / qwa_profile_end): marks around a main kernel launch
+void profile_mark_begin(hipStream_t st);
+void profile_mark_end(hipStream_t st);
+
 hipError_t launch_prep(const qwa_row_src& qg, const qwa_row_src& k, const qwa_row_src& v, const float* qn,
                        const float* kn, int pos0, int rpos0, int n, float theta, float eps, int kvt,
                        const qwa_kv_layer& kv, float* q_out, float* gate, hipStream_t st);

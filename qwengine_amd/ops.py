@@ -73,6 +73,8 @@ EXPORTS = {
                                 [ctypes.c_int] * 3 + [ctypes.c_void_p] * 2),
     "qwa_kv_append": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.c_int] * 3 + [ctypes.POINTER(_KVLayerC),
                                                                                   ctypes.c_void_p]),
+    "qwa_profile_begin": (ctypes.c_int, []),
+    "qwa_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
     "qwa_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "qwa_last_error": (ctypes.c_char_p, []),
 }
@@ -279,6 +281,19 @@ def attn_prefill_simple(q, gate, kv: KVLayer, kvt, B: int, p0: int, out16, strea
     """src/cuda/prefill.cuh:61-62."""
     _check(lib().qwa_attn_prefill_simple(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), B, p0, _ptr(out16),
                                          _stream(stream)))
+
+
+def profile_begin() -> None:
+    """Start timing the main kernel of every attention call (HIP events around each launch)."""
+    _check(lib().qwa_profile_begin())
+
+
+def profile_end() -> tuple[float, int]:
+    """Stop timing; returns (summed main-kernel time in ms, number of timed launches)."""
+    ms = ctypes.c_double(0.0)
+    n = ctypes.c_int(0)
+    _check(lib().qwa_profile_end(ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value
 
 
 def kv_append(xk, xv, pos0: int, n: int, kvt, kv: KVLayer, stream=None) -> None:
