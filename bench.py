@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--positions", type=int, default=150000)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="headline decode only")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run 5 device copies of 512 MiB (a known-size kernel to calibrate HBM counters)")
     return ap.parse_args()
 
 
@@ -114,6 +116,13 @@ def main():
     kern_ms, kern_n = ops.profile_end()
     kern_us = kern_ms * 1000.0 / max(kern_n, 1)
     us_layer = ms_per_step * 1000.0 / L
+    if args.copy_probe:
+        src = torch.empty(1 << 27, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     bytes_layer = n * BYTES_PER_POS[kvt]
     gbs = bytes_layer / (us_layer * 1e-6) / 1e9
 
