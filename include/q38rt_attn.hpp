@@ -5,6 +5,7 @@
 // Like the reference, a rejected call prints the reason and aborts (src/cuda/ops.cu:1002-1008).
 #pragma once
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
@@ -134,6 +135,17 @@ inline void attn_prefill_simple(const float* q, const float* gate, const KVLayer
                                 uint16_t* out16, hipStream_t st) {
     const qwa_kv_layer l = detail::c(kv);
     detail::check(qwa_attn_prefill_simple(q, gate, &l, (int)kvt, B, p0, out16, st), "attn_prefill_simple");
+}
+
+// the engine passes its fp16 output buffer as __half* (src/runtime/engine.cpp:2479)
+inline void attn_prefill(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int B, int p0,
+                         __half* out16, hipStream_t st) {
+    attn_prefill(q, gate, kv, kvt, B, p0, reinterpret_cast<uint16_t*>(out16), st);
+}
+
+inline void attn_prefill_simple(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int B, int p0,
+                                __half* out16, hipStream_t st) {
+    attn_prefill_simple(q, gate, kv, kvt, B, p0, reinterpret_cast<uint16_t*>(out16), st);
 }
 
 }  // namespace cuda

@@ -104,7 +104,8 @@ int main() {
     void (*fp)(const float*, const float*, const KVLayer&, KVType, int, int, void*, float*, const ActQ8*,
                hipStream_t, float*) = attn_decode_multi;
     void (*pp)(const float*, const float*, const KVLayer&, KVType, int, int, uint16_t*, hipStream_t) = attn_prefill;
-    return (fp && pp) ? 0 : 3;
+    void (*ph)(const float*, const float*, const KVLayer&, KVType, int, int, __half*, hipStream_t) = attn_prefill;
+    return (fp && pp && ph) ? 0 : 3;
 }
 '''
     tmp = os.path.join(ROOT, "_build_test_shim")
