@@ -26,7 +26,7 @@ sys.path.insert(0, HERE)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 METRIC = "decode attn µs/layer + HBM GB/s @150K Q4_0 KV; prefill attn TFLOP/s (1024-tok chunk)"
-# HBM bytes per k_dec launch at the headline workload, measured with rocprofv3 PMC counters (read 173.2 MB + write
+# HBM bytes per k_dec4 launch at the headline workload, measured with rocprofv3 PMC counters (read 173.2 MB + write
 # 3.19 MB; the kernel's algorithmic bytes are 172.8 MB)
 KDEC_TRAFFIC = 176.4e6
 BYTES_PER_POS = {0: 4096, 1: 2176, 2: 1152}  # K + V values and scales over the 4 KV heads
@@ -150,8 +150,8 @@ def main():
                      "frac": round(bytes_layer / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "traffic": KDEC_TRAFFIC if (n, L) == (150000, 16) else None,
                      "traffic_source": "rocprofv3 --pmc FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), calibrated on a "
-                                       "512 MiB copy, per k_dec dispatch",
-                     "kernel": "k_dec (split-K decode), average over the timed launches",
+                                       "512 MiB copy, per k_dec4 dispatch",
+                     "kernel": "k_dec4 (split-K Q4_0 decode), average over the timed launches",
                      "kernel_us": round(kern_us, 3), "launches": kern_n,
                      "algorithmic_bytes_per_launch": bytes_layer},
     }

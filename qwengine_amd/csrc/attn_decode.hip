@@ -153,6 +153,51 @@ __device__ __forceinline__ void fold(float& m, float& l, f4* o, float m2, float 
     m = M;
 }
 
+// LDS of the cross-wave merge (aliases the chunk rings once streaming is over)
+struct MergeLds {
+    f4 o[2][16][64];
+    float ml[2][2][64];
+};
+
+// Merges the partial states (m, l, O) of the 4 waves of a workgroup as fold(fold(c0, c1), fold(c2, c3)); returns
+// true in wave 0, which then holds the merged state.  Every wave must call it (it synchronises the workgroup).
+__device__ __forceinline__ bool merge4(MergeLds& s, int wave, int lane, float& m, float& l, f4* o) {
+    __syncthreads();  // every wave is done with the ring (or with the previous merge)
+    if (wave & 1) {
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) s.o[wave >> 1][dt][lane] = o[dt];
+        s.ml[wave >> 1][0][lane] = m;
+        s.ml[wave >> 1][1][lane] = l;
+    }
+    __syncthreads();
+    if (!(wave & 1)) {
+        f4 o2[16];
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) o2[dt] = s.o[wave >> 1][dt][lane];
+        fold(m, l, o, s.ml[wave >> 1][0][lane], s.ml[wave >> 1][1][lane], o2);
+    }
+    __syncthreads();
+    if (wave == 2) {
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) s.o[0][dt][lane] = o[dt];
+        s.ml[0][0][lane] = m;
+        s.ml[0][1][lane] = l;
+    }
+    __syncthreads();
+    if (wave != 0) return false;
+    f4 o2[16];
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++) o2[dt] = s.o[0][dt][lane];
+    fold(m, l, o, s.ml[0][0][lane], s.ml[0][1][lane], o2);
+    return true;
+}
+
+// sum over the 4 lanes l % 16 + 16 k that hold one row
+__device__ __forceinline__ float half4_sum(float x) {
+    x += __shfl_xor(x, 16, 64);
+    return x + __shfl_xor(x, 32, 64);
+}
+
 // ring depth (chunks in flight per wave): sized so that two 4-wave workgroups fit a CU's 160 KB of LDS where possible
 template <int KVT, int RT> struct DecCfg {
     static constexpr int NST = KVT == QWA_KV_Q4_0 ? (RT == 1 ? 3 : 2) : 1;
@@ -168,10 +213,7 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     // the chunk ring of every wave while streaming; two partial states while merging
     __shared__ __attribute__((aligned(16))) union {
         uint8_t ring[WG_CLASSES][NST][C::BYTES];
-        struct {
-            f4 o[2][16][64];
-            float ml[2][2][64];
-        } merge;
+        MergeLds merge;
     } s_u;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
@@ -334,40 +376,10 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     // ---- merge the 4 classes as fold(fold(c0, c1), fold(c2, c3)) per row tile; wave 0 writes the records
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
-        __syncthreads();  // every wave is done with the ring (or with the previous tile's merge)
-        if (wave & 1) {
-#pragma unroll
-            for (int dt = 0; dt < 16; dt++) s_u.merge.o[wave >> 1][dt][lane] = o[rt][dt];
-            s_u.merge.ml[wave >> 1][0][lane] = m[rt];
-            s_u.merge.ml[wave >> 1][1][lane] = l[rt];
-        }
-        __syncthreads();
-        if (!(wave & 1)) {
-            f4 o2[16];
-#pragma unroll
-            for (int dt = 0; dt < 16; dt++) o2[dt] = s_u.merge.o[wave >> 1][dt][lane];
-            fold(m[rt], l[rt], o[rt], s_u.merge.ml[wave >> 1][0][lane], s_u.merge.ml[wave >> 1][1][lane], o2);
-        }
-        __syncthreads();
-        if (wave == 2) {
-#pragma unroll
-            for (int dt = 0; dt < 16; dt++) s_u.merge.o[0][dt][lane] = o[rt][dt];
-            s_u.merge.ml[0][0][lane] = m[rt];
-            s_u.merge.ml[0][1][lane] = l[rt];
-        }
-        __syncthreads();
-        if (wave == 0) {
-            {
-                f4 o2[16];
-#pragma unroll
-                for (int dt = 0; dt < 16; dt++) o2[dt] = s_u.merge.o[0][dt][lane];
-                fold(m[rt], l[rt], o[rt], s_u.merge.ml[0][0][lane], s_u.merge.ml[0][1][lane], o2);
-            }
-            float lt = l[rt];
-            lt += __shfl_xor(lt, 16, 64);
-            lt += __shfl_xor(lt, 32, 64);
+        if (merge4(s_u.merge, wave, lane, m[rt], l[rt], o[rt])) {
             const int r = 16 * (rt0 + rt) + i16;
             const int qt = r / GRP, hh = r % GRP;
+            const float lt = half4_sum(l[rt]);
             if (qpos[rt] >= 0) {
                 float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt) * GRP + hh) * REC;
                 if (lg == 0) {
@@ -388,6 +400,317 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     }
 }
 
+// ---------------------------------------------------------------------------------------------- Q4_0 decode
+// The same split-K structure as k_dec, with an inner loop laid out for Q4_0 to keep the vector ALU work per KV byte
+// low (the kernel has to issue ~4.6 KB of dequantisation and softmax per 16-key chunk at HBM rate):
+//  * K and V both sit piece-major in LDS (16-byte piece = one 32-value block of one key): the S^T operand read is one
+//    dword per block, and the P.V operand gathers byte m of a block for 4 keys from dwords that 4 lanes read together
+//    (broadcast) plus one per-lane byte select per key pair;
+//  * fp16 codes come from one and-or per pair (exponent trick: 0x6400 | n is 1024 + n, 0x5400 | (n << 4) is 64 + n)
+//    and one exact packed subtraction; V is scaled by its fp16 block scale with one rounding (= fp16(d * (n - 8)));
+//  * P.V runs as two 16-dim tiles per block (even and odd dims) that share the lane's 4 keys' block scales;
+//  * full chunks load from uniform base addresses with per-lane constant offsets; only the chunk holding the
+//    window's last key takes the clamped path;
+//  * the softmax only rescales when some score of the chunk exceeds the running maximum by more than RESCALE_T
+//    (one compare and a wave vote in the common case).
+// Chunk image in LDS (bytes):
+//   [0, 2048)    K values: block b of key n at (16 b + n) * 16
+//   [2048, 4096) V values, same layout
+//   [4096, 4352) K block scales, [key][8] fp16
+//   [4352, 4608) V block scales, [key][8] fp16
+struct Q4Chunk {
+    static constexpr int K = 0, V = 2048, KS = 4096, VS = 4352, BYTES = 4608;
+    static constexpr int NLOAD = 6;  // load instructions per chunk
+};
+
+// per-lane source offsets (bytes from the chunk's first row) of the K / V piece loads of a full chunk: instruction i,
+// lane l fills slot 64 i + l = piece 4 i + l / 16 of row l % 16
+struct Q4Offsets {
+    uint32_t piece[2];
+};
+
+__device__ __forceinline__ Q4Offsets q4_offsets(int lane) {
+    Q4Offsets o;
+#pragma unroll
+    for (int i = 0; i < 2; i++) o.piece[i] = (lane & 15) * 128 + 16 * (4 * i + (lane >> 4));
+    return o;
+}
+
+// Direct-to-LDS loads written as inline asm: the compiler's wait-count pass would otherwise treat every later LDS
+// read as possibly reading the in-flight DMA data and wait for all outstanding loads (vmcnt(0)), which serialises the
+// chunk ring.  The kernel orders them itself: s_waitcnt vmcnt before reading a slot, lgkmcnt(0) before refilling it.
+// LDS destination = m0 + lane * size; source = scalar base + per-lane 32-bit offset (or a per-lane 64-bit address).
+// An SALU write of m0 needs one wait state before an LDS DMA reads it (the s_nop).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <int SIZE>
+__device__ __forceinline__ void dma_sv(uint32_t lds, const void* sbase, uint32_t voff) {
+    if constexpr (SIZE == 16)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
+    else if constexpr (SIZE == 4)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_ushort %1, %2" ::"s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
+}
+template <int SIZE>
+__device__ __forceinline__ void dma_v(uint32_t lds, const void* addr) {
+    if constexpr (SIZE == 16)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
+    else if constexpr (SIZE == 4)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_ushort %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+
+__device__ __forceinline__ void q4_issue_full(uint32_t dst, const qwa_kv_layer& kv, size_t row0, const Q4Offsets& off,
+                                              int lane) {
+    const uint8_t* kb = kv.k + row0 * 128;
+    const uint8_t* vb = kv.v + row0 * 128;
+    const uint16_t* ksb = kv.ks + row0 * 8;
+    const uint16_t* vsb = kv.vs + row0 * 8;
+    dma_sv<16>(dst + Q4Chunk::K, kb, off.piece[0]);
+    dma_sv<16>(dst + Q4Chunk::K + 1024, kb, off.piece[1]);
+    dma_sv<16>(dst + Q4Chunk::V, vb, off.piece[0]);
+    dma_sv<16>(dst + Q4Chunk::V + 1024, vb, off.piece[1]);
+    dma_sv<4>(dst + Q4Chunk::KS, ksb, 4 * lane);
+    dma_sv<4>(dst + Q4Chunk::VS, vsb, 4 * lane);
+}
+
+// the chunk holding key kmax: rows past kmax re-read row kmax (their scores are masked, their probabilities are 0)
+__device__ __forceinline__ void q4_issue_tail(uint32_t dst, const qwa_kv_layer& kv, size_t rowbase, int kb, int kmax,
+                                              int lane) {
+    const size_t rk = rowbase + min(kb + (lane & 15), kmax);
+    const int pc = 16 * (lane >> 4);
+    dma_v<16>(dst + Q4Chunk::K, kv.k + rk * 128 + pc);
+    dma_v<16>(dst + Q4Chunk::K + 1024, kv.k + rk * 128 + pc + 64);
+    dma_v<16>(dst + Q4Chunk::V, kv.v + rk * 128 + pc);
+    dma_v<16>(dst + Q4Chunk::V + 1024, kv.v + rk * 128 + pc + 64);
+    const size_t rs = rowbase + min(kb + (lane >> 2), kmax);
+    dma_v<4>(dst + Q4Chunk::KS, reinterpret_cast<const uint8_t*>(kv.ks + rs * 8) + 4 * (lane & 3));
+    dma_v<4>(dst + Q4Chunk::VS, reinterpret_cast<const uint8_t*>(kv.vs + rs * 8) + 4 * (lane & 3));
+}
+
+// Bit masks / fp16 exponent patterns of the code unpacking, held in VGPRs so that each (x & mask) | pattern is one
+// v_and_or_b32 (VOP3 encodings take no 32-bit literals on this target).
+struct Q4Masks {
+    uint32_t lo, hi, e_lo, e_hi;
+};
+__device__ __forceinline__ Q4Masks q4_masks() {
+    Q4Masks k;
+    asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(k.lo));
+    asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(k.hi));
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(k.e_lo));
+    asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(k.e_hi));
+    return k;
+}
+
+// 8 Q4_0 codes (one dword: block elements 8 g .. 8 g + 7, element 2 j in the low nibble of byte j) as exact fp16
+// integers n - 8 in the order [e0, e4, e1, e5, e2, e6, e3, e7] (k_perm<Q4_0>)
+__device__ __forceinline__ h8 q4_codes(uint32_t w, const Q4Masks& k) {
+    const h2 b_lo = {(_Float16)1032.0f, (_Float16)1032.0f}, b_hi = {(_Float16)72.0f, (_Float16)72.0f};
+    const uint32_t w8 = w >> 8;
+    const uint32_t e04 = h2_bits(bits_h2((w & k.lo) | k.e_lo) - b_lo);
+    const uint32_t e15 = h2_bits(bits_h2((w & k.hi) | k.e_hi) - b_hi);
+    const uint32_t e26 = h2_bits(bits_h2((w8 & k.lo) | k.e_lo) - b_lo);
+    const uint32_t e37 = h2_bits(bits_h2((w8 & k.hi) | k.e_hi) - b_hi);
+    return make_h8(e04, e15, e26, e37);
+}
+
+template <int NST>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work) {
+    __shared__ __attribute__((aligned(16))) union {
+        uint8_t ring[WG_CLASSES][NST][Q4Chunk::BYTES];
+        MergeLds merge;
+    } s_u;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int i16 = lane & 15, lg = lane >> 4;
+    const int g = blockIdx.y, rec = blockIdx.x;
+    const int kmax = pos0 + nq - 1;
+    const int nchunk = kmax / CHUNK + 1;
+    const int cls = rec * WG_CLASSES + wave;
+    const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;
+    const size_t rowbase = (size_t)g * kv.capacity;
+
+    // Q / 16 as fp16 hi + lo, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + k_perm(j)
+    h8 qh[8], ql[8];
+    const int r = 16 * rt0 + i16;
+    const int qt = r / GRP, hh = r % GRP;
+    const int qpos = qt < nq ? pos0 + qt : -1;  // last visible key of this lane's row (-1: padding row)
+    {
+        const float* src = q + ((size_t)(qt < nq ? qt : 0) * NH + g * GRP + hh) * HD + 8 * lg;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const float4 a = *reinterpret_cast<const float4*>(src + 32 * b);
+            const float4 c = *reinterpret_cast<const float4*>(src + 32 * b + 4);
+            const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float v = qt < nq ? x[k_perm<QWA_KV_Q4_0>(j)] * 0.0625f : 0.0f;
+                qh[b][j] = (_Float16)v;
+                ql[b][j] = (_Float16)(v - (float)qh[b][j]);
+            }
+        }
+    }
+    f4 o[16];
+#pragma unroll
+    for (int t = 0; t < 16; t++) o[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    float msl = 0.0f;        // m * log2(e), 0 while m = -inf
+    float mthr = -INFINITY;  // m + RESCALE_T
+
+    if (nmine > 0) {
+        uint8_t(*ring)[Q4Chunk::BYTES] = s_u.ring[wave];
+        const Q4Offsets off = q4_offsets(lane);
+        const Q4Masks km = q4_masks();
+        const uint32_t bsel = (uint32_t)(i16 & 3) | 0x0c000c00u | ((uint32_t)(4 + (i16 & 3)) << 16);
+        auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * j); };
+        auto issue = [&](int j) {
+            const int kb = chunk_key(j);
+            const uint32_t dst = lds_addr(ring[j % NST]);
+            if (kb + CHUNK - 1 <= kmax) q4_issue_full(dst, kv, rowbase + kb, off, lane);
+            else q4_issue_tail(dst, kv, rowbase, kb, kmax, lane);
+        };
+        // K of chunk j from LDS: the 8 code dwords of this lane and the block scales of its 4 keys
+        struct KRegs {
+            uint32_t w[8];
+            uint32_t d[4][4];
+        };
+        auto read_k = [&](int j, KRegs& r) {
+            const uint8_t* cst = ring[j % NST];
+#pragma unroll
+            for (int b = 0; b < 8; b++)
+                r.w[b] = *reinterpret_cast<const uint32_t*>(cst + Q4Chunk::K + (16 * b + i16) * 16 + 4 * lg);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint4 u = *reinterpret_cast<const uint4*>(cst + Q4Chunk::KS + (4 * lg + i) * 16);
+                r.d[i][0] = u.x; r.d[i][1] = u.y; r.d[i][2] = u.z; r.d[i][3] = u.w;
+            }
+        };
+        // V of chunk j: byte i16 of block b for keys 4 lg + {0, 2} / {1, 3} as {byte, 0, byte, 0} (the 4 lanes of a
+        // dword read it together, a per-lane byte select picks each lane's byte), and the keys' block scales
+        struct VRegs {
+            uint32_t x02[8], x13[8];
+            uint32_t d[4][4];
+        };
+        auto read_v = [&](int j, VRegs& r) {
+            const uint8_t* cst = ring[j % NST];
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const uint32_t* vp =
+                    reinterpret_cast<const uint32_t*>(cst + Q4Chunk::V + (16 * b + 4 * lg) * 16 + (i16 & 12));
+                r.x02[b] = __builtin_amdgcn_perm(vp[8], vp[0], bsel);
+                r.x13[b] = __builtin_amdgcn_perm(vp[12], vp[4], bsel);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint4 u = *reinterpret_cast<const uint4*>(cst + Q4Chunk::VS + (4 * lg + i) * 16);
+                r.d[i][0] = u.x; r.d[i][1] = u.y; r.d[i][2] = u.z; r.d[i][3] = u.w;
+            }
+        };
+        // S^T of one chunk: per block the exact integer codes times Q_hi + Q_lo, times the key's block scale
+        auto scores = [&](const KRegs& r) {
+            f4 S = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const h8 ka = q4_codes(r.w[b], km);
+                f4 a = mfma16(ka, qh[b], f4{0.0f, 0.0f, 0.0f, 0.0f});
+                a = mfma16(ka, ql[b], a);
+#pragma unroll
+                for (int i = 0; i < 4; i++) S[i] = fmaf(h2f_bits((uint16_t)(r.d[i][b >> 1] >> (16 * (b & 1)))), a[i], S[i]);
+            }
+            return S;
+        };
+        // online softmax of chunk j (lane: keys kb + 4 lg + i of row i16) -> P^T operand, keys {0, 2}, {1, 3}
+        auto softmax = [&](int j, f4 S) {
+            const int kb = chunk_key(j);
+            float sv[4] = {S[0], S[1], S[2], S[3]};
+            if (kb + CHUNK - 1 > pos0) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) sv[i] = kb + 4 * lg + i <= qpos ? sv[i] : -INFINITY;
+            }
+            const float mx4 = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            if (__any(mx4 > mthr)) {
+                const float mx = row_max4(mx4);
+                const float mn = mx > mthr ? mx : m;
+                const float cr = mn == m ? 1.0f : fast_exp2((m - mn) * LOG2E);  // m = -inf: cr = 0
+                if (__any(cr != 1.0f)) {
+#pragma unroll
+                    for (int t = 0; t < 16; t++) o[t] *= cr;
+                    l *= cr;
+                }
+                m = mn;
+                msl = mn == -INFINITY ? 0.0f : mn * LOG2E;
+                mthr = mn + RESCALE_T;
+            }
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) p[i] = fast_exp2(fmaf(sv[i], LOG2E, -msl));
+            const h2 p02 = {(_Float16)p[0], (_Float16)p[2]}, p13 = {(_Float16)p[1], (_Float16)p[3]};
+            const h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+            l = __builtin_amdgcn_fdot2(p13, one2, __builtin_amdgcn_fdot2(p02, one2, l, false), false);
+            return make_h4(h2_bits(p02), h2_bits(p13));
+        };
+        // O^T += V^T P^T: block b as two 16-dim tiles, even dims (tile 2 b) and odd dims (tile 2 b + 1); the lane
+        // (dim pair i16, group lg) holds keys in the order {4 lg, 4 lg + 2, 4 lg + 1, 4 lg + 3}
+        auto pv = [&](const VRegs& r, h4 P) {
+            const h2 b_lo = {(_Float16)1032.0f, (_Float16)1032.0f}, b_hi = {(_Float16)72.0f, (_Float16)72.0f};
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const uint32_t sel = (b & 1) ? 0x07060302u : 0x05040100u;  // halfword b & 1 of both words
+                const h2 d02 = bits_h2(__builtin_amdgcn_perm(r.d[2][b >> 1], r.d[0][b >> 1], sel));
+                const h2 d13 = bits_h2(__builtin_amdgcn_perm(r.d[3][b >> 1], r.d[1][b >> 1], sel));
+                const uint32_t e02 = h2_bits((bits_h2((r.x02[b] & km.lo) | km.e_lo) - b_lo) * d02);
+                const uint32_t e13 = h2_bits((bits_h2((r.x13[b] & km.lo) | km.e_lo) - b_lo) * d13);
+                const uint32_t f02 = h2_bits((bits_h2((r.x02[b] & km.hi) | km.e_hi) - b_hi) * d02);
+                const uint32_t f13 = h2_bits((bits_h2((r.x13[b] & km.hi) | km.e_hi) - b_hi) * d13);
+                o[2 * b] = mfma16k16(make_h4(e02, e13), P, o[2 * b]);
+                o[2 * b + 1] = mfma16k16(make_h4(f02, f13), P, o[2 * b + 1]);
+            }
+        };
+
+#pragma unroll
+        for (int st = 0; st < NST; st++)
+            if (st < nmine) issue(st);
+        for (int j = 0; j < nmine; j++) {
+            if (j + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
+            else wait_vmcnt<0>();
+            KRegs kr;
+            read_k(j, kr);
+            VRegs vr;
+            read_v(j, vr);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot j is read out: refill it
+            if (j + NST < nmine) issue(j + NST);
+            const h4 P = softmax(j, scores(kr));
+            pv(vr, P);
+        }
+    }
+
+    // ---- merge the 4 classes; wave 0 writes the records.  Lane (row i16, lg), tile 2 b + par, element i holds
+    // dim 32 b + 8 lg + 2 i + par.
+    if (merge4(s_u.merge, wave, lane, m, l, o)) {
+        const float lt = half4_sum(l);
+        if (qpos >= 0) {
+            float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt) * GRP + hh) * REC;
+            if (lg == 0) {
+                recp[0] = m;
+                recp[1] = lt;
+            }
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                float* dst = recp + 4 + 32 * b + 8 * lg;
+                *reinterpret_cast<float4*>(dst) = make_float4(o[2 * b][0], o[2 * b + 1][0], o[2 * b][1], o[2 * b + 1][1]);
+                *reinterpret_cast<float4*>(dst + 4) =
+                    make_float4(o[2 * b][2], o[2 * b + 1][2], o[2 * b][3], o[2 * b + 1][3]);
+            }
+        }
+    }
+}
+
 // Combine: one workgroup per (query t, head h, quarter of the head dims).  256 threads = 64 dims x 4 slices.
 // Sums run over fixed groups of CGRP consecutive splits, in split order inside a group and in group order across
 // groups: the summation tree depends only on split indices, never on nq (splits past a query's window hold l = 0
@@ -396,54 +719,64 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
                                                      const float* __restrict__ gate, float* __restrict__ out,
                                                      float* __restrict__ out_host, qwa_act_q8 oq, int do_q) {
     constexpr int MAXSPLIT = NREC;
-    constexpr int MAXGRP = (MAXSPLIT + CGRP - 1) / CGRP;
+    constexpr int MAXGRP = MAXSPLIT / CGRP;
+    constexpr int GPS = MAXGRP / 4;  // groups per slice
     __shared__ float s_f[MAXSPLIT];
-    __shared__ float s_l[MAXSPLIT];
-    __shared__ float s_red[8];
+    __shared__ float s_lf[MAXSPLIT];
     __shared__ float s_gl[MAXGRP];
+    __shared__ float s_red[4];
     __shared__ float s_ga[MAXGRP][64];
     const int t = blockIdx.x / NH, h = blockIdx.x % NH, g = h / GRP, hh = h % GRP;
     const int quarter = blockIdx.y;
     const int tid = threadIdx.x, dim = tid & 63, slice = tid >> 6;
     const size_t sstride = (size_t)NKV * MAXQ * GRP * REC;
     const float* base = work + (((size_t)g * MAXQ + t) * GRP + hh) * REC;
+    const int d = 64 * quarter + dim;
 
-    // global max over splits that saw keys
-    float mx = -INFINITY;
-    for (int s = tid; s < nsplit; s += 256) {
-        const float ls = base[s * sstride + 1];
-        const float ms = base[s * sstride];
-        s_l[s] = ls;
-        s_f[s] = ms;
-        if (ls > 0.0f) mx = fmaxf(mx, ms);
+    // every load up front: this thread's O values (groups slice, slice + 4, ...) and one record's (m, l)
+    float ov[GPS][CGRP];
+#pragma unroll
+    for (int k = 0; k < GPS; k++)
+#pragma unroll
+        for (int i = 0; i < CGRP; i++) {
+            const int s = (slice + 4 * k) * CGRP + i;
+            ov[k][i] = s < nsplit ? base[s * sstride + 4 + d] : 0.0f;
+        }
+    float ms = -INFINITY, ls = 0.0f;
+    if (tid < nsplit) {
+        ms = base[tid * sstride];
+        ls = base[tid * sstride + 1];
     }
-    mx = wave_max(mx);
+    // global max over records that saw keys, then each record's factor exp(m - M) (0 for empty records)
+    float mx = wave_max(ls > 0.0f ? ms : -INFINITY);
     if ((tid & 63) == 0) s_red[tid >> 6] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    for (int s = tid; s < nsplit; s += 256) s_f[s] = s_l[s] > 0.0f ? __expf(s_f[s] - M) : 0.0f;
-    __syncthreads();
-
-    const int ngrp = (nsplit + CGRP - 1) / CGRP;
-    // group partial sums of l * f (one thread per group) and of O * f (slice per group, round robin)
-    if (tid < ngrp) {
-        float L = 0.0f;
-        const int s1 = min(nsplit, (tid + 1) * CGRP);
-        for (int s = tid * CGRP; s < s1; s++) L += s_l[s] * s_f[s];
-        s_gl[tid] = L;
+    const float f = ls > 0.0f ? __expf(ms - M) : 0.0f;
+    if (tid < MAXSPLIT) {
+        s_f[tid] = f;
+        s_lf[tid] = ls * f;
     }
-    const int d = 64 * quarter + dim;
-    for (int gr = slice; gr < ngrp; gr += 4) {
+    __syncthreads();
+    // L and A: sums over fixed groups of CGRP records, in record order inside a group and group order across groups
+    if (tid < MAXGRP) {
+        float Lg = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CGRP; i++) Lg += s_lf[tid * CGRP + i];
+        s_gl[tid] = Lg;
+    }
+#pragma unroll
+    for (int k = 0; k < GPS; k++) {
+        const int gr = slice + 4 * k;
         float A = 0.0f;
-        const int s1 = min(nsplit, (gr + 1) * CGRP);
-#pragma unroll 8
-        for (int s = gr * CGRP; s < s1; s++) A += base[s * sstride + 4 + d] * s_f[s];
+#pragma unroll
+        for (int i = 0; i < CGRP; i++) A += ov[k][i] * s_f[gr * CGRP + i];
         s_ga[gr][dim] = A;
     }
     __syncthreads();
     if (slice != 0) return;
     float L = 0.0f, A = 0.0f;
-    for (int gr = 0; gr < ngrp; gr++) {
+    for (int gr = 0; gr < MAXGRP; gr++) {
         L += s_gl[gr];
         A += s_ga[gr][dim];
     }
@@ -474,7 +807,12 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
                            hipStream_t st) {
     const int rt = (GRP * nq + 15) / 16;
     const dim3 grid(nrec, NKV);
-    for (int t = 0; t < rt; t++) hipLaunchKernelGGL((k_dec<KVT, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
+    for (int t = 0; t < rt; t++) {
+        if constexpr (KVT == QWA_KV_Q4_0)
+            hipLaunchKernelGGL((k_dec4<3>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
+        else
+            hipLaunchKernelGGL((k_dec<KVT, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
+    }
 }
 
 hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int pos0, int nq,
