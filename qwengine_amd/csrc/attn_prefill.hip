@@ -24,6 +24,7 @@ constexpr int PF_TILE = 64;                      // keys per tile
 constexpr int KS_LD = HD + 8;                    // K tile row stride (halves): conflict-free 16-byte reads
 constexpr int VT_LD = PF_TILE + 8;               // V^T tile row stride (halves)
 constexpr float PF_LOG2E = 1.4426950408889634f;
+constexpr float PF_RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maximum (natural-log units)
 
 // raw bytes of one tile held by one thread between the global load and the LDS store
 template <int KVT> struct PfRaw {
@@ -40,44 +41,36 @@ template <int KVT> struct PfRaw {
 // half cb / 4, lane group cb % 4), dims 8 (t / 8) .. + 8
 template <int KVT>
 __device__ __forceinline__ void pf_load(PfRaw<KVT>& r, const qwa_kv_layer& kv, size_t rowbase, int k0, int kmax) {
+    // keys past kmax re-read row kmax: their scores are masked (p = 0) and the row holds finite values, so the loads
+    // need no branches
     constexpr int VB = value_bytes(KVT);
     constexpr int P = VB / 16;
     const int t = threadIdx.x;
 #pragma unroll
     for (int c = 0; c < PfRaw<KVT>::KP; c++) {
-        const int idx = t + 256 * c, key = k0 + idx / P, pc = idx % P;
-        if (key <= kmax) {
-            const size_t row = rowbase + key;
-            r.k[c] = ld16(kv.k + row * VB + 16 * pc);
-            if (KVT == QWA_KV_Q4_0) r.ks[c] = kv.ks[row * 8 + pc];
-            else if (KVT == QWA_KV_Q8_0) r.ks[c] = kv.ks[row * 8 + (pc >> 1)];
-        } else {
-            r.k[c] = make_uint4(0, 0, 0, 0);
-            r.ks[c] = 0;
-        }
+        const int idx = t + 256 * c, key = min(k0 + idx / P, kmax), pc = idx % P;
+        const size_t row = rowbase + key;
+        r.k[c] = ld16(kv.k + row * VB + 16 * pc);
+        if (KVT == QWA_KV_Q4_0) r.ks[c] = kv.ks[row * 8 + pc];
+        else if (KVT == QWA_KV_Q8_0) r.ks[c] = kv.ks[row * 8 + (pc >> 1)];
+        else r.ks[c] = 0;
     }
     const int cb = t & 7, dc = t >> 3, h32 = cb >> 2, gq = cb & 3;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        const int key = k0 + 32 * h32 + (j < 4 ? 4 * gq + j : 16 + 4 * gq + (j - 4));
-        if (key <= kmax) {
-            const size_t row = rowbase + key;
-            const uint8_t* p = kv.v + row * VB + (VB / 32) * dc;
-            if constexpr (KVT == QWA_KV_Q4_0) {
-                r.v[j][0] = *reinterpret_cast<const uint32_t*>(p);
-            } else if constexpr (KVT == QWA_KV_Q8_0) {
-                const uint2 u = ld8(p);
-                r.v[j][0] = u.x; r.v[j][1] = u.y;
-            } else {
-                const uint4 u = ld16(p);
-                r.v[j][0] = u.x; r.v[j][1] = u.y; r.v[j][2] = u.z; r.v[j][3] = u.w;
-            }
-            r.vs[j] = KVT == QWA_KV_F16 ? 0 : kv.vs[row * 8 + (dc >> 2)];
+        const int key = min(k0 + 32 * h32 + (j < 4 ? 4 * gq + j : 16 + 4 * gq + (j - 4)), kmax);
+        const size_t row = rowbase + key;
+        const uint8_t* p = kv.v + row * VB + (VB / 32) * dc;
+        if constexpr (KVT == QWA_KV_Q4_0) {
+            r.v[j][0] = *reinterpret_cast<const uint32_t*>(p);
+        } else if constexpr (KVT == QWA_KV_Q8_0) {
+            const uint2 u = ld8(p);
+            r.v[j][0] = u.x; r.v[j][1] = u.y;
         } else {
-#pragma unroll
-            for (int i = 0; i < PfRaw<KVT>::VW; i++) r.v[j][i] = 0;
-            r.vs[j] = 0;
+            const uint4 u = ld16(p);
+            r.v[j][0] = u.x; r.v[j][1] = u.y; r.v[j][2] = u.z; r.v[j][3] = u.w;
         }
+        r.vs[j] = KVT == QWA_KV_F16 ? 0 : kv.vs[row * 8 + (dc >> 2)];
     }
 }
 
@@ -168,24 +161,27 @@ k_prefill(const float* __restrict__ q, const float* __restrict__ gate, qwa_kv_la
     const int wave_qmin = p0 + wrow0 / GRP;
 
     f4 o[PF_RT][16];
-    float m[PF_RT], l[PF_RT];
+    float m[PF_RT], l[PF_RT], msl[PF_RT], mthr[PF_RT];
 #pragma unroll
     for (int rt = 0; rt < PF_RT; rt++) {
         m[rt] = -INFINITY;
         l[rt] = 0.0f;
+        msl[rt] = 0.0f;
+        mthr[rt] = -INFINITY;
 #pragma unroll
         for (int dt = 0; dt < 16; dt++) o[rt][dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
+    // raw bytes of tile kt + 1 are in registers while tile kt is computed; they are dequantised into the other LDS
+    // buffer in the same straight-line block as tile kt's MFMAs, and tile kt + 2 is loaded right after
     PfRaw<KVT> raw;
     pf_load<KVT>(raw, kv, rowbase, 0, kmax);
     pf_store<KVT>(raw, s_k[0], s_vt[0]);
+    pf_load<KVT>(raw, kv, rowbase, min(1, n_tiles - 1) * PF_TILE, kmax);
     __syncthreads();
 
     for (int kt = 0; kt < n_tiles; kt++) {
         const int k0 = kt * PF_TILE, buf = kt & 1;
-        const bool more = kt + 1 < n_tiles;
-        if (more) pf_load<KVT>(raw, kv, rowbase, k0 + PF_TILE, kmax);
         const _Float16* Ks = s_k[buf];
         const _Float16* Vt = s_vt[buf];
 
@@ -204,49 +200,57 @@ k_prefill(const float* __restrict__ q, const float* __restrict__ gate, qwa_kv_la
             }
         }
 
-        // ---- mask + online softmax (lane: row (rt, i16), keys k0 + 16 k4 + 4 lg + i)
+        // ---- mask + online softmax (lane: row (rt, i16), keys k0 + 16 k4 + 4 lg + i).  The reference maximum m
+        // moves only when a score exceeds it by more than PF_RESCALE_T (probabilities stay <= e^PF_RESCALE_T, far
+        // inside fp16), so the accumulators are rarely rescaled.
         const bool need_mask = k0 + PF_TILE - 1 > wave_qmin;
         h8 pb[PF_RT][2];
+        float cr[PF_RT];
 #pragma unroll
         for (int rt = 0; rt < PF_RT; rt++) {
-            float mx = -INFINITY;
             if (need_mask) {
 #pragma unroll
                 for (int k4 = 0; k4 < 4; k4++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const int key = k0 + 16 * k4 + 4 * lg + i;
-                        if (key > qpos[rt]) sc[rt][k4][i] = -INFINITY;
+                        sc[rt][k4][i] = key > qpos[rt] ? -INFINITY : sc[rt][k4][i];
                     }
             }
+            float mx = -INFINITY;
 #pragma unroll
             for (int k4 = 0; k4 < 4; k4++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[rt][k4][i]);
+                mx = fmaxf(mx, fmaxf(fmaxf(sc[rt][k4][0], sc[rt][k4][1]), fmaxf(sc[rt][k4][2], sc[rt][k4][3])));
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = fmaxf(m[rt], mx);
-            const float msl = (mn == -INFINITY ? 0.0f : mn) * PF_LOG2E;
-            const float c = fast_exp2(m[rt] * PF_LOG2E - msl);
+            const float mn = mx > mthr[rt] ? mx : m[rt];
+            cr[rt] = mn == m[rt] ? 1.0f : fast_exp2((m[rt] - mn) * PF_LOG2E);  // m = -inf: c = 0
+            m[rt] = mn;
+            msl[rt] = mn == -INFINITY ? 0.0f : mn * PF_LOG2E;
+            mthr[rt] = mn + PF_RESCALE_T;
             float rs = 0.0f;
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
                 h8 p;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const float e = fast_exp2(fmaf(sc[rt][2 * ks + (j >> 2)][j & 3], PF_LOG2E, -msl));
+                    const float e = fast_exp2(fmaf(sc[rt][2 * ks + (j >> 2)][j & 3], PF_LOG2E, -msl[rt]));
                     rs += e;
                     p[j] = (_Float16)e;
                 }
                 pb[rt][ks] = p;
             }
-            l[rt] = l[rt] * c + rs;
-            m[rt] = mn;
+            l[rt] = l[rt] * cr[rt] + rs;
+        }
+        if (__any(cr[0] != 1.0f || cr[PF_RT - 1] != 1.0f)) {
 #pragma unroll
-            for (int dt = 0; dt < 16; dt++) o[rt][dt] *= c;
+            for (int rt = 0; rt < PF_RT; rt++)
+#pragma unroll
+                for (int dt = 0; dt < 16; dt++) o[rt][dt] *= cr[rt];
         }
 
-        // ---- O^T += V^T P^T: 16 dim tiles x 2 key steps of 32
+        // ---- O^T += V^T P^T: 16 dim tiles x 2 key steps of 32; meanwhile tile kt + 1 is dequantised into the
+        // other buffer (the last iteration writes a copy that is never read)
 #pragma unroll
         for (int dt = 0; dt < 16; dt++) {
             const _Float16* vr = Vt + (16 * dt + i16) * VT_LD + 8 * lg;
@@ -257,8 +261,8 @@ k_prefill(const float* __restrict__ q, const float* __restrict__ gate, qwa_kv_la
                 for (int rt = 0; rt < PF_RT; rt++) o[rt][dt] = mfma16(a, pb[rt][ks], o[rt][dt]);
             }
         }
-
-        if (more) pf_store<KVT>(raw, s_k[buf ^ 1], s_vt[buf ^ 1]);
+        pf_store<KVT>(raw, s_k[buf ^ 1], s_vt[buf ^ 1]);
+        pf_load<KVT>(raw, kv, rowbase, min(kt + 2, n_tiles - 1) * PF_TILE, kmax);
         __syncthreads();
     }
 
