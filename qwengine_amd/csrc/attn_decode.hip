@@ -59,7 +59,6 @@ __host__ __device__ constexpr int kpos(int row, int byte) {
     return ((byte >> 4) * CHUNK + row) * 16 + (byte & 15);
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
 
 // Direct-to-LDS loads of one chunk (16 B per lane per instruction: K piece-major, V row-major, then the scales).
 // Rows past kmax re-read row kmax (no read outside the window; their scores are masked and their probabilities are
@@ -87,11 +86,6 @@ __device__ __forceinline__ void issue_chunk(uint8_t* dst, const qwa_kv_layer& kv
     }
 }
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 // A operand of block b for lane (key n, group g): exact integers (no scale), dims 32 b + 8 g + perm(j)
 template <int KVT>
@@ -436,34 +430,6 @@ __device__ __forceinline__ Q4Offsets q4_offsets(int lane) {
     return o;
 }
 
-// Direct-to-LDS loads written as inline asm: the compiler's wait-count pass would otherwise treat every later LDS
-// read as possibly reading the in-flight DMA data and wait for all outstanding loads (vmcnt(0)), which serialises the
-// chunk ring.  The kernel orders them itself: s_waitcnt vmcnt before reading a slot, lgkmcnt(0) before refilling it.
-// LDS destination = m0 + lane * size; source = scalar base + per-lane 32-bit offset (or a per-lane 64-bit address).
-// An SALU write of m0 needs one wait state before an LDS DMA reads it (the s_nop).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-template <int SIZE>
-__device__ __forceinline__ void dma_sv(uint32_t lds, const void* sbase, uint32_t voff) {
-    if constexpr (SIZE == 16)
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
-    else if constexpr (SIZE == 4)
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
-    else
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_ushort %1, %2" ::"s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
-}
-template <int SIZE>
-__device__ __forceinline__ void dma_v(uint32_t lds, const void* addr) {
-    if constexpr (SIZE == 16)
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
-    else if constexpr (SIZE == 4)
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
-    else
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_ushort %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
 
 __device__ __forceinline__ void q4_issue_full(uint32_t dst, const qwa_kv_layer& kv, size_t row0, const Q4Offsets& off,
                                               int lane) {

@@ -1,17 +1,22 @@
 // Causal prefill attention over the quantized KV cache on fp16 MFMA (gfx950).
 //
-// FlashAttention-2 structure (the reference's k_attn_prefill_mma, src/cuda/prefill.cu:522-794, re-designed for
-// wave64 / MFMA / 160 KB LDS):
-//  * a workgroup owns 128 consecutive (query, head) rows of one KV head (row r = 6 * token + head) and walks the
-//    causal key range in 32-key tiles; 4 consumer waves own 32 rows each (two 16-row MFMA tiles);
-//  * 4 producer waves (one per SIMD) stage the tiles: the raw quantized K/V bytes of tile kt + 2 sit in their
-//    registers while tile kt + 1 is dequantized to fp16 into the other half of a double buffer in LDS -- K as
-//    [key][dim], V transposed as [dim][key] so both MFMA A-operands are single 16-byte LDS reads; one barrier per
-//    tile.  The role branch keeps the two register sets apart, so the consumers keep Q, S, P and O in registers;
-//  * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16 (fp32 accumulation); each K / V fragment read from
-//    LDS feeds both row tiles of the wave;  P^T comes out of the S^T accumulator already in B-operand layout;
-//  * online softmax in fp32 (exp2 with log2 e folded in), lazy rescale, deferred 1/l, fused sigmoid gate, fp16 out.
-//  32-key tiles keep the consumer at 256 VGPRs (two waves per SIMD); 64-key tiles spill.
+// FlashAttention-2 structure (the reference's k_attn_prefill_mma, src/cuda/prefill.cu:522-794), laid out for how
+// gfx950 issues work: a wave's VALU instructions do not overlap its own MFMAs, and every 16-byte LDS operand read
+// costs matrix-pipe issue time, so
+//  * each SIMD runs two MFMA waves (8 waves, 512 threads per workgroup): one wave's softmax / dequantisation VALU work
+//    issues while the other's MFMAs run; a wave owns 32 (query, head) rows (two 16-row MFMA tiles), so every K / V
+//    fragment read from LDS feeds two MFMAs; a workgroup owns 256 consecutive rows of one KV head
+//    (row r = 6 * token + head);
+//  * keys are walked in 32-key tiles.  The raw quantized bytes of a tile go HBM -> LDS by direct-to-LDS loads
+//    (no registers) two tiles ahead; all threads then dequantise the next tile cooperatively into fp16 LDS tiles, K as
+//    [key][dim] and V transposed as [dim][key], so both MFMA A-operands are single 16-byte LDS reads; one barrier per
+//    tile;
+//  * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16 (fp32 accumulation); P^T comes out of the S^T
+//    accumulator already in B-operand layout; online softmax in fp32 with a lazy rescale;
+//  * the causal key range of a row block is cut into PF_NS fixed splits (one workgroup each) so that the
+//    96 row blocks x 4 KV heads of a 1024-token chunk fill the chip; each split leaves a partial state (m, l, O) in
+//    a library-owned device buffer and k_pf_combine merges the splits in a fixed order, normalises, applies the
+//    sigmoid gate and writes fp16.  Chunks longer than PF_MAXB tokens run as several passes.
 #include <float.h>
 
 #include "kv_operands.hpp"
@@ -19,91 +24,119 @@
 
 namespace qwa {
 
-#ifndef QWA_PF_CW
-#define QWA_PF_CW 4
+#ifndef QWA_PF_WAVES
+#define QWA_PF_WAVES 8
 #endif
-constexpr int PF_CWAVES = QWA_PF_CW;             // consumer (MFMA) waves
-constexpr int PF_PWAVES = 4;                     // producer (staging) waves, one per SIMD
-constexpr int PF_PT = PF_PWAVES * 64;            // producer threads
-constexpr int PF_THREADS = (PF_CWAVES + PF_PWAVES) * 64;
-constexpr int PF_RT = 8 / PF_CWAVES;             // 16-row MFMA tiles per consumer wave
-constexpr int PF_ROWS = PF_CWAVES * PF_RT * 16;  // 128 rows per workgroup
-#ifndef QWA_PF_TILE
-#define QWA_PF_TILE 32
-#endif
-constexpr int PF_TILE = QWA_PF_TILE;             // keys per tile
+constexpr int PF_WAVES = QWA_PF_WAVES;           // MFMA waves per workgroup
+constexpr int PF_THREADS = PF_WAVES * 64;
+constexpr int PF_WPE = PF_WAVES / 4;             // waves per SIMD
+constexpr int PF_RT = 16 / PF_WAVES;             // 16-row MFMA tiles per wave
+constexpr int PF_ROWS = PF_WAVES * PF_RT * 16;   // 256 rows per workgroup
+constexpr int PF_TILE = 32;                      // keys per tile
 constexpr int PF_KT = PF_TILE / 16;              // 16-key MFMA tiles per tile
-constexpr int PF_KS = PF_TILE / 32;              // 32-key P.V steps per tile
-constexpr int PF_CB = PF_TILE / 8;               // V column blocks (8 key positions each)
-constexpr int KS_LD = HD + 8;                    // K tile row stride (halves): conflict-free 16-byte reads
+constexpr int PF_NS = 8;                         // key-range splits per row block
+constexpr int PF_MAXB = 1024;                    // tokens per pass
+constexpr int PF_MAXROWS = PF_MAXB * NH;         // output rows per pass
+constexpr int KS_LD = HD + 8;                    // K tile row stride (halves)
 constexpr int VT_LD = PF_TILE + 8;               // V^T tile row stride (halves)
+#ifndef QWA_PF_VD
+#define QWA_PF_VD 3
+#endif
+constexpr int PF_VD = QWA_PF_VD;                 // V fragments in flight
+#ifndef QWA_PF_GROUP_BIT
+#define QWA_PF_GROUP_BIT 4
+#endif
+constexpr int PF_GROUP_BIT = QWA_PF_GROUP_BIT;   // wave bit that tells the two waves of a SIMD apart
 constexpr float PF_LOG2E = 1.4426950408889634f;
 constexpr float PF_RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maximum (natural-log units)
 
-// raw bytes of one tile held by one thread between the global load and the LDS store
+// Partial softmax states of one pass: unnormalised O [split][row][HD] and (m, l) [split][row], row = token * NH +
+// head.  Library-owned (about 200 MB of device memory), so attn_prefill keeps the reference's signature without a
+// work buffer; calls that overlap on one device share it and must be stream-ordered.
+__device__ float4 pf_part_o[(size_t)PF_NS * PF_MAXROWS * HD / 4];
+__device__ float2 pf_part_ml[PF_NS * PF_MAXROWS];
+
+// raw bytes of one tile in LDS, in the cache's own layout: K rows, V rows, K scales, V scales (8 fp16 per row)
 template <int KVT> struct PfRaw {
     static constexpr int VB = value_bytes(KVT);
-    static constexpr int KP = PF_TILE * (VB / 16) / PF_PT;   // 16-byte K pieces per producer thread
-    static constexpr int VR = PF_TILE / 32;                  // V (8 keys x 4 dims) groups per producer thread
-    static constexpr int VW = KVT == QWA_KV_F16 ? 2 : 1;     // V words per key for 4 dims
-    uint4 k[KP];
-    uint16_t ks[KP];
-    uint32_t v[VR][8][VW];
-    uint16_t vs[VR][8];
+    static constexpr int K = 0, V = PF_TILE * VB;
+    static constexpr int SC = KVT == QWA_KV_F16 ? 0 : PF_TILE * 16;
+    static constexpr int KS = 2 * PF_TILE * VB, VS = KS + SC;
+    static constexpr int BYTES = 2 * PF_TILE * VB + 2 * SC;
+    static constexpr int NKV = PF_TILE * VB / 1024;          // 1 KB load instructions for K (and for V)
+    static constexpr int NBUF = KVT == QWA_KV_F16 ? 2 : 3;   // raw tiles in flight (F16 tiles are 32 KB)
+    static constexpr int AHEAD = NBUF - 1;                    // tiles loaded ahead of the one being computed
+    // load instructions of wave w per tile: K instruction i on wave i % W, V instruction i on wave (i + W / 2) % W,
+    // K scales (two 256-byte instructions) on waves W - 2, W - 1, V scales on waves W / 2 - 2, W / 2 - 1
+    __device__ static constexpr int count(int w) {
+        int n = 0;
+        for (int i = 0; i < NKV; i++) n += (i % PF_WAVES == w) + ((i + PF_WAVES / 2) % PF_WAVES == w);
+        if (SC) n += (w >= PF_WAVES - 2) + (w >= PF_WAVES / 2 - 2 && w < PF_WAVES / 2);
+        return n;
+    }
 };
 
-// producer thread t (of 256): K pieces idx = t + 256 c (key idx / P, piece idx % P); V: for each rep the position
-// tt = t + 256 rep gives column block cb = tt % PF_CB (keys of the 32-key step cb / 4, lane group cb % 4) and dims
-// 4 (tt / PF_CB) .. + 4.  Keys past kmax re-read row kmax: their scores are masked (p = 0) and the row holds finite
-// values, so the loads need no branches.
+// Issues this wave's direct-to-LDS loads of the tile starting at key k0: K instructions wave, wave + 8, ..., V
+// instructions (wave + 4) % 8, + 8, ..., scales on waves 2, 3 (V) and 6, 7 (K).  Keys past kmax re-read row kmax
+// (they are masked, and no read leaves the window).  wave is wave-uniform.
 template <int KVT>
-__device__ __forceinline__ void pf_load(PfRaw<KVT>& r, const qwa_kv_layer& kv, size_t rowbase, int k0, int kmax,
-                                        int t) {
-    constexpr int VB = value_bytes(KVT);
-    constexpr int P = VB / 16;
+__device__ __forceinline__ void pf_issue(uint32_t raw, const qwa_kv_layer& kv, size_t rowbase, int k0, int kmax,
+                                         int wave, int lane) {
+    using L = PfRaw<KVT>;
+    constexpr int VB = L::VB;
+    const int kn = kmax - k0;  // last valid key of the tile, relative
+    const uint8_t* kb = kv.k + (rowbase + k0) * VB;
+    const uint8_t* vb = kv.v + (rowbase + k0) * VB;
 #pragma unroll
-    for (int c = 0; c < PfRaw<KVT>::KP; c++) {
-        const int idx = t + PF_PT * c, key = min(k0 + idx / P, kmax), pc = idx % P;
-        const size_t row = rowbase + key;
-        r.k[c] = ld16(kv.k + row * VB + 16 * pc);
-        if (KVT == QWA_KV_Q4_0) r.ks[c] = kv.ks[row * 8 + pc];
-        else if (KVT == QWA_KV_Q8_0) r.ks[c] = kv.ks[row * 8 + (pc >> 1)];
-        else r.ks[c] = 0;
-    }
-#pragma unroll
-    for (int rep = 0; rep < PfRaw<KVT>::VR; rep++) {
-        const int tt = t + PF_PT * rep, cb = tt % PF_CB, dc = tt / PF_CB, h32 = cb >> 2, gq = cb & 3;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int key = min(k0 + 32 * h32 + (j < 4 ? 4 * gq + j : 16 + 4 * gq + (j - 4)), kmax);
-            const size_t row = rowbase + key;
-            if constexpr (KVT == QWA_KV_Q4_0) {
-                r.v[rep][j][0] = *reinterpret_cast<const uint16_t*>(kv.v + row * VB + 2 * dc);  // 4 dims = 2 bytes
-            } else if constexpr (KVT == QWA_KV_Q8_0) {
-                r.v[rep][j][0] = *reinterpret_cast<const uint32_t*>(kv.v + row * VB + 4 * dc);
-            } else {
-                const uint2 u = ld8(kv.v + row * VB + 8 * dc);
-                r.v[rep][j][0] = u.x;
-                r.v[rep][j][1] = u.y;
-            }
-            r.vs[rep][j] = KVT == QWA_KV_F16 ? 0 : kv.vs[row * 8 + (dc >> 3)];
+    for (int c = 0; c < (L::NKV + PF_WAVES - 1) / PF_WAVES; c++) {
+        const int ik = wave + PF_WAVES * c, iv = (wave + PF_WAVES / 2) % PF_WAVES + PF_WAVES * c;
+        if (ik < L::NKV) {
+            const int p = 1024 * ik + 16 * lane;
+            dma_sv<16>(raw + L::K + 1024 * ik, kb, (uint32_t)(min(p / VB, kn) * VB + p % VB));
         }
+        if (iv < L::NKV) {
+            const int p = 1024 * iv + 16 * lane;
+            dma_sv<16>(raw + L::V + 1024 * iv, vb, (uint32_t)(min(p / VB, kn) * VB + p % VB));
+        }
+    }
+    if constexpr (L::SC != 0) {
+        // lane l: dword l % 4 of the 8 scales of key 16 j + l / 4
+        const int j = wave & 1;
+        const uint32_t off = (uint32_t)(min(16 * j + lane / 4, kn) * 16 + 4 * (lane & 3));
+        if (wave >= PF_WAVES - 2) dma_sv<4>(raw + L::KS + 256 * j, kv.ks + (rowbase + k0) * 8, off);
+        if (wave >= PF_WAVES / 2 - 2 && wave < PF_WAVES / 2)
+            dma_sv<4>(raw + L::VS + 256 * j, kv.vs + (rowbase + k0) * 8, off);
+    }
+}
+
+// waits until at most n of this wave's direct-to-LDS loads are outstanding (n is wave-uniform)
+__device__ __forceinline__ void wait_vm(int n) {
+    switch (n) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<1>(); break;
+        case 2: wait_vmcnt<2>(); break;
+        case 3: wait_vmcnt<3>(); break;
+        case 4: wait_vmcnt<4>(); break;
+        case 5: wait_vmcnt<5>(); break;
+        case 6: wait_vmcnt<6>(); break;
+        default: wait_vmcnt<0>(); break;
     }
 }
 
 // 4 dims of one V key as two half2 {d0, d1}, {d2, d3}, scaled by the key's block scale (one fp16 rounding)
 template <int KVT>
-__device__ __forceinline__ void pf_v4(const uint32_t* w, uint32_t sc, uint32_t* out) {
+__device__ __forceinline__ void pf_v4(const uint8_t* vrow, int dc, uint32_t sc, uint32_t* out) {
     if constexpr (KVT == QWA_KV_F16) {
-        out[0] = w[0];
-        out[1] = w[1];
+        const uint2 u = *reinterpret_cast<const uint2*>(vrow + 8 * dc);
+        out[0] = u.x;
+        out[1] = u.y;
     } else if constexpr (KVT == QWA_KV_Q8_0) {
         const h2 d = scale_pair((uint16_t)sc, (uint16_t)sc);
-        q8_word_to_h4(w[0], d, out);
+        q8_word_to_h4(*reinterpret_cast<const uint32_t*>(vrow + 4 * dc), d, out);
     } else {
         const h2 d = scale_pair((uint16_t)sc, (uint16_t)sc);
         const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
-        const uint32_t x = w[0];
+        const uint32_t x = *reinterpret_cast<const uint16_t*>(vrow + 2 * dc);
         // byte 0 -> dims 0 (low nibble), 1 (high nibble); byte 1 -> dims 2, 3
         const uint32_t p01 = ((x & 0x0Fu) | ((x & 0xF0u) << 12)) | 0x64006400u;
         const uint32_t p23 = (((x >> 8) & 0x0Fu) | (((x >> 8) & 0xF0u) << 12)) | 0x64006400u;
@@ -112,26 +145,43 @@ __device__ __forceinline__ void pf_v4(const uint32_t* w, uint32_t sc, uint32_t* 
     }
 }
 
+// Dequantises one raw tile into the fp16 tiles (thread t of 512).  K: LDS position 32 s + 8 g + j of a row holds dim
+// 32 s + 8 g + perm(j) (the Q operand is loaded with the same permutation).  V^T: row d, position 8 cb + j holds key
+// 16 (j / 4) + 4 cb + j % 4, the key order of the P^T operand (lane group g of a 16-key MFMA tile holds keys
+// 4 g .. 4 g + 3).
 template <int KVT>
-__device__ __forceinline__ void pf_store(const PfRaw<KVT>& r, _Float16* Ks, _Float16* Vt, int t) {
-    constexpr int VB = value_bytes(KVT);
-    constexpr int P = VB / 16;
+__device__ __forceinline__ void pf_convert_kv(const uint8_t* raw, _Float16* Ks, _Float16* Vt, int t, bool do_k,
+                                              bool do_v) {
+    using L = PfRaw<KVT>;
+    constexpr int VB = L::VB;
+    const uint16_t* kss = reinterpret_cast<const uint16_t*>(raw + L::KS);
+    const uint16_t* vss = reinterpret_cast<const uint16_t*>(raw + L::VS);
+    if (!do_k) {
+    } else if constexpr (KVT == QWA_KV_F16) {
 #pragma unroll
-    for (int c = 0; c < PfRaw<KVT>::KP; c++) {
-        const int idx = t + PF_PT * c, key = idx / P, pc = idx % P;
-        const uint4 u = r.k[c];
+        for (int c = 0; c < 2; c++) {
+            const int idx = t + 512 * c, key = idx >> 5, pc = idx & 31;
+            *reinterpret_cast<uint4*>(Ks + key * KS_LD + 8 * pc) =
+                *reinterpret_cast<const uint4*>(raw + L::K + key * VB + 16 * pc);
+        }
+    } else if constexpr (KVT == QWA_KV_Q8_0) {
+        const int key = t >> 4, pc = t & 15;
+        const uint4 u = *reinterpret_cast<const uint4*>(raw + L::K + key * VB + 16 * pc);
+        const uint16_t sc = kss[key * 8 + (pc >> 1)];
+        const h2 d = scale_pair(sc, sc);
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-        if constexpr (KVT == QWA_KV_F16) {
-            *reinterpret_cast<uint4*>(Ks + key * KS_LD + 8 * pc) = u;
-        } else if constexpr (KVT == QWA_KV_Q8_0) {
-            const h2 d = scale_pair(r.ks[c], r.ks[c]);
-            uint32_t o[8];
+        uint32_t o[8];
 #pragma unroll
-            for (int i = 0; i < 4; i++) q8_word_to_h4(w[i], d, o + 2 * i);
-            *reinterpret_cast<uint4*>(Ks + key * KS_LD + 16 * pc) = make_uint4(o[0], o[1], o[2], o[3]);
-            *reinterpret_cast<uint4*>(Ks + key * KS_LD + 16 * pc + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-        } else {
-            const h2 d = scale_pair(r.ks[c], r.ks[c]);
+        for (int i = 0; i < 4; i++) q8_word_to_h4(w[i], d, o + 2 * i);
+        *reinterpret_cast<uint4*>(Ks + key * KS_LD + 16 * pc) = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4*>(Ks + key * KS_LD + 16 * pc + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+    } else {
+        if (t < PF_TILE * 8) {
+            const int key = t >> 3, pc = t & 7;
+            const uint4 u = *reinterpret_cast<const uint4*>(raw + L::K + key * VB + 16 * pc);
+            const uint16_t sc = kss[key * 8 + pc];
+            const h2 d = scale_pair(sc, sc);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 uint32_t o[4];
@@ -140,81 +190,95 @@ __device__ __forceinline__ void pf_store(const PfRaw<KVT>& r, _Float16* Ks, _Flo
             }
         }
     }
-    // V^T: row (dim) 4 dc + d, positions 8 cb .. 8 cb + 7
+    if (!do_v) return;
+    // V^T: thread (cb, dc, h) converts keys 16 h + 4 cb + jj (jj < 4), dims 4 dc .. 4 dc + 3
+    const int cb = t & 3, dc = (t >> 2) & 63, h = t >> 8;
+    uint32_t hv[4][2];
 #pragma unroll
-    for (int rep = 0; rep < PfRaw<KVT>::VR; rep++) {
-        const int tt = t + PF_PT * rep, cb = tt % PF_CB, dc = tt / PF_CB;
-        uint32_t hv[8][2];  // [key position][dim pair]
-#pragma unroll
-        for (int j = 0; j < 8; j++) pf_v4<KVT>(r.v[rep][j], r.vs[rep][j], hv[j]);
-#pragma unroll
-        for (int d = 0; d < 4; d++) {
-            uint32_t w[4];
-            const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;  // high / low half of both words
-#pragma unroll
-            for (int jp = 0; jp < 4; jp++)
-                w[jp] = __builtin_amdgcn_perm(hv[2 * jp + 1][d >> 1], hv[2 * jp][d >> 1], sel);
-            *reinterpret_cast<uint4*>(Vt + (4 * dc + d) * VT_LD + 8 * cb) = make_uint4(w[0], w[1], w[2], w[3]);
-        }
+    for (int jj = 0; jj < 4; jj++) {
+        const int key = 16 * h + 4 * cb + jj;
+        const uint32_t sc = KVT == QWA_KV_F16 ? 0u : (uint32_t)vss[key * 8 + (dc >> 3)];
+        pf_v4<KVT>(raw + L::V + key * VB, dc, sc, hv[jj]);
     }
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;  // high / low half of both words
+        const uint32_t w0 = __builtin_amdgcn_perm(hv[1][d >> 1], hv[0][d >> 1], sel);
+        const uint32_t w1 = __builtin_amdgcn_perm(hv[3][d >> 1], hv[2][d >> 1], sel);
+        *reinterpret_cast<uint2*>(Vt + (4 * dc + d) * VT_LD + 8 * cb + 4 * h) = make_uint2(w0, w1);
+    }
+}
+
+// 512 threads convert K and V; 1024 threads split them (threads 0-511 K, 512-1023 V)
+template <int KVT>
+__device__ __forceinline__ void pf_convert(const uint8_t* raw, _Float16* Ks, _Float16* Vt, int t) {
+    if constexpr (PF_THREADS == 512) pf_convert_kv<KVT>(raw, Ks, Vt, t, true, true);
+    else pf_convert_kv<KVT>(raw, Ks, Vt, t & 511, t < 512, t >= 512);
 }
 
 __device__ __forceinline__ h8 lds_h8(const _Float16* p) { return *reinterpret_cast<const h8*>(p); }
 
+// max of three floats in one instruction (fmaxf would first canonicalize each MFMA result; scores are never sNaN)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// max / sum over the four 16-lane rows of the wave (lanes l, l ^ 16, l ^ 32, l ^ 48) with the gfx950 lane swaps:
+// permlane16_swap(x, x) leaves row pairs {r0, r0, r2, r2} / {r1, r1, r3, r3}, permlane32_swap {lo, lo} / {hi, hi}
+__device__ __forceinline__ float rows_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    float y;
+    asm("v_max_f32 %0, %1, %2" : "=v"(y) : "v"(__uint_as_float(a[0])), "v"(__uint_as_float(a[1])));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    asm("v_max_f32 %0, %1, %2" : "=v"(y) : "v"(__uint_as_float(b[0])), "v"(__uint_as_float(b[1])));
+    return y;
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// One split of one row block: grid (row blocks, NKV, PF_NS).  Tokens 0 .. B-1 of this pass sit at cache positions
+// p0 .. p0 + B - 1.
 template <int KVT>
-__global__ void __launch_bounds__(PF_THREADS)
-__attribute__((amdgpu_waves_per_eu(PF_THREADS / 256, PF_THREADS / 256)))
-k_prefill(const float* __restrict__ q, const float* __restrict__ gate, qwa_kv_layer kv, int B, int p0,
-          uint16_t* __restrict__ out16) {
+__global__ void __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(PF_WPE, PF_WPE)))
+k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0) {
+    using L = PfRaw<KVT>;
+    __shared__ __attribute__((aligned(16))) uint8_t s_raw[L::NBUF][L::BYTES];
     __shared__ __attribute__((aligned(16))) _Float16 s_k[2][PF_TILE * KS_LD];
     __shared__ __attribute__((aligned(16))) _Float16 s_vt[2][HD * VT_LD];
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
-    const bool producer = wave >= PF_CWAVES;
-    const int pt = threadIdx.x - PF_CWAVES * 64;  // producer thread index
-    const int i16 = lane & 15, lg = lane >> 4;
-    const int g = blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63, i16 = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(t >> 6));
+    const int g = blockIdx.y, sp = blockIdx.z;
     const int row0 = blockIdx.x * PF_ROWS;
     const int nrows = GRP * B;
-    // last key any row of the workgroup sees; tiles past it are never needed
+    // last key any row of the workgroup sees, and this split's tiles [tb, tb + nt) of the row block's range
     const int last_row = min(row0 + PF_ROWS, nrows) - 1;
     const int kmax = p0 + last_row / GRP;
     const int n_tiles = kmax / PF_TILE + 1;
+    const int tb = sp * n_tiles / PF_NS, nt = (sp + 1) * n_tiles / PF_NS - tb;
     const size_t rowbase = (size_t)g * kv.capacity;
+    const int nvm = L::count(wave);
+    uint32_t raw_lds[L::NBUF];
+#pragma unroll
+    for (int b = 0; b < L::NBUF; b++) raw_lds[b] = lds_addr(s_raw[b]);
 
-    if (producer) {
-        // staging waves: the raw bytes of tile kt + 2 are in registers while the consumers compute tile kt; tile
-        // kt + 1 is dequantised into the other buffer meanwhile (the last iteration writes a copy that is never read).
-        // The role branch encloses each role's whole state, so the two register sets never overlap.
-        PfRaw<KVT> raw;
-        pf_load<KVT>(raw, kv, rowbase, 0, kmax, pt);
-        pf_store<KVT>(raw, s_k[0], s_vt[0], pt);
-        pf_load<KVT>(raw, kv, rowbase, min(1, n_tiles - 1) * PF_TILE, kmax, pt);
-        __syncthreads();
-        for (int kt = 0; kt < n_tiles; kt++) {
-            const int buf = kt & 1;
-            pf_store<KVT>(raw, s_k[buf ^ 1], s_vt[buf ^ 1], pt);
-            pf_load<KVT>(raw, kv, rowbase, min(kt + 2, n_tiles - 1) * PF_TILE, kmax, pt);
-            __syncthreads();
-        }
-        return;
-    }
-
-    // ---- consumer (MFMA) waves
-    // this lane's rows: token tq, head hh, last visible key qpos
-    int tq[PF_RT], hh[PF_RT], qpos[PF_RT];
+    // this lane's rows (token r / 6, head r % 6) and last visible key qpos; Q / 16 as the fp16 B operand
+    int qpos[PF_RT];
     h8 qb[PF_RT][8];
     const int wrow0 = row0 + 16 * PF_RT * wave;
 #pragma unroll
     for (int rt = 0; rt < PF_RT; rt++) {
-        const int r = wrow0 + 16 * rt + i16;
-        tq[rt] = r / GRP;
-        hh[rt] = r % GRP;
-        const bool valid = tq[rt] < B;
-        qpos[rt] = valid ? p0 + tq[rt] : -1;
-        const float* qrow = q + ((size_t)(valid ? tq[rt] : 0) * NH + g * GRP + hh[rt]) * HD;
+        const int r = wrow0 + 16 * rt + i16, tq = r / GRP, hh = r % GRP;
+        const bool valid = tq < B;
+        qpos[rt] = valid ? p0 + tq : -1;
+        const float* qrow = q + ((size_t)(valid ? tq : 0) * NH + g * GRP + hh) * HD;
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-            // LDS position 32 s + 8 lg + j of a K row holds dim 32 s + 8 lg + perm(j)
             const float* src = qrow + 32 * s + 8 * lg;
             const float4 a = *reinterpret_cast<const float4*>(src);
             const float4 b = *reinterpret_cast<const float4*>(src + 4);
@@ -229,143 +293,210 @@ k_prefill(const float* __restrict__ q, const float* __restrict__ gate, qwa_kv_la
     const int wave_qmin = p0 + wrow0 / GRP;
 
     f4 o[PF_RT][16];
-    float m[PF_RT], l[PF_RT], msl[PF_RT], mthr[PF_RT];
+    float m[PF_RT], l[PF_RT];
 #pragma unroll
     for (int rt = 0; rt < PF_RT; rt++) {
         m[rt] = -INFINITY;
         l[rt] = 0.0f;
-        msl[rt] = 0.0f;
-        mthr[rt] = -INFINITY;
 #pragma unroll
         for (int dt = 0; dt < 16; dt++) o[rt][dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    __syncthreads();  // tile 0 staged
-
-    for (int kt = 0; kt < n_tiles; kt++) {
-        const int k0 = kt * PF_TILE, buf = kt & 1;
-        const _Float16* Ks = s_k[buf];
-        const _Float16* Vt = s_vt[buf];
-
-        // ---- S^T = K Q^T for PF_KT key tiles of 16
-        f4 sc[PF_RT][PF_KT];
+    if (nt > 0) {
+        // prologue: raw tiles 0 .. AHEAD - 1 in flight, tile 0 dequantised (and, with AHEAD >= 2, tile 1 landed)
+        wait_vmcnt<0>();  // the Q loads; from here on vmcnt counts only the tile loads
 #pragma unroll
-        for (int k4 = 0; k4 < PF_KT; k4++)
-#pragma unroll
-            for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-#pragma unroll
-            for (int k4 = 0; k4 < PF_KT; k4++) {
-                const h8 a = lds_h8(Ks + (16 * k4 + i16) * KS_LD + 8 * lg + 32 * s);
-#pragma unroll
-                for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = mfma16(a, qb[rt][s], sc[rt][k4]);
-            }
-        }
-
-        // ---- mask + online softmax (lane: row (rt, i16), keys k0 + 16 k4 + 4 lg + i).  The reference maximum m
-        // moves only when a score exceeds it by more than PF_RESCALE_T (probabilities stay <= e^PF_RESCALE_T, far
-        // inside fp16), so the accumulators are rarely rescaled.
-        const bool need_mask = k0 + PF_TILE - 1 > wave_qmin;
-        h8 pb[PF_RT][PF_KS];
-        float cr[PF_RT];
-#pragma unroll
-        for (int rt = 0; rt < PF_RT; rt++) {
-            if (need_mask) {
-#pragma unroll
-                for (int k4 = 0; k4 < PF_KT; k4++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int key = k0 + 16 * k4 + 4 * lg + i;
-                        sc[rt][k4][i] = key > qpos[rt] ? -INFINITY : sc[rt][k4][i];
-                    }
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int k4 = 0; k4 < PF_KT; k4++)
-                mx = fmaxf(mx, fmaxf(fmaxf(sc[rt][k4][0], sc[rt][k4][1]), fmaxf(sc[rt][k4][2], sc[rt][k4][3])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = mx > mthr[rt] ? mx : m[rt];
-            cr[rt] = mn == m[rt] ? 1.0f : fast_exp2((m[rt] - mn) * PF_LOG2E);  // m = -inf: c = 0
-            m[rt] = mn;
-            msl[rt] = mn == -INFINITY ? 0.0f : mn * PF_LOG2E;
-            mthr[rt] = mn + PF_RESCALE_T;
-            float rs = 0.0f;
-#pragma unroll
-            for (int ks = 0; ks < PF_KS; ks++) {
-                h8 p;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float e = fast_exp2(fmaf(sc[rt][2 * ks + (j >> 2)][j & 3], PF_LOG2E, -msl[rt]));
-                    rs += e;
-                    p[j] = (_Float16)e;
-                }
-                pb[rt][ks] = p;
-            }
-            l[rt] = l[rt] * cr[rt] + rs;
-        }
-        if (__any(cr[0] != 1.0f || cr[PF_RT - 1] != 1.0f)) {
-#pragma unroll
-            for (int rt = 0; rt < PF_RT; rt++)
-#pragma unroll
-                for (int dt = 0; dt < 16; dt++) o[rt][dt] *= cr[rt];
-        }
-
-        // ---- O^T += V^T P^T: 16 dim tiles x PF_KS key steps of 32; dim tile dt + 1's fragments are read while dt
-        // multiplies
-        {
-            h8 cur[PF_KS], nxt[PF_KS];
-#pragma unroll
-            for (int ks = 0; ks < PF_KS; ks++) nxt[ks] = lds_h8(Vt + i16 * VT_LD + 8 * lg + 32 * ks);
-#pragma unroll
-            for (int dt = 0; dt < 16; dt++) {
-#pragma unroll
-                for (int ks = 0; ks < PF_KS; ks++) cur[ks] = nxt[ks];
-                if (dt < 15) {
-#pragma unroll
-                    for (int ks = 0; ks < PF_KS; ks++) nxt[ks] = lds_h8(Vt + (16 * (dt + 1) + i16) * VT_LD + 8 * lg + 32 * ks);
-                }
-#pragma unroll
-                for (int ks = 0; ks < PF_KS; ks++)
-#pragma unroll
-                    for (int rt = 0; rt < PF_RT; rt++) o[rt][dt] = mfma16(cur[ks], pb[rt][ks], o[rt][dt]);
-            }
-        }
-
+        for (int i = 0; i < L::AHEAD; i++)
+            pf_issue<KVT>(raw_lds[i], kv, rowbase, (tb + min(i, nt - 1)) * PF_TILE, kmax, wave, lane);
+        wait_vm(nvm * (L::AHEAD - 1));
+        __syncthreads();
+        pf_convert<KVT>(s_raw[0], s_k[0], s_vt[0], t);
+        if constexpr (L::AHEAD >= 2) wait_vm(nvm * (L::AHEAD - 2));
         __syncthreads();
     }
 
-    // ---- normalise, gate, fp16 out: lane holds dims 16 dt + 4 lg + i of row (rt, i16)
+    // The two waves of a SIMD (w and w + 4) run the phases of a tile in different orders so that one issues VALU /
+    // LDS work (dequantisation, softmax) while the other's MFMAs run:
+    //   waves 0-3: convert | S       | softmax | PV
+    //   waves 4-7: S       | softmax | PV      | convert
+    const bool lead = (wave & PF_GROUP_BIT) == 0;
+    for (int i = 0; i < nt; i++) {
+        const int k0 = (tb + i) * PF_TILE, cur = i & 1;
+        // tile i + AHEAD (the last tile again near the end: a harmless re-read) into the raw buffer freed last
+        // iteration
+        pf_issue<KVT>(raw_lds[(i + L::AHEAD) % L::NBUF], kv, rowbase, (tb + min(i + L::AHEAD, nt - 1)) * PF_TILE,
+                      kmax, wave, lane);
+        const _Float16* Ks = s_k[cur];
+        const _Float16* Vt = s_vt[cur];
+
+        // the next tile's raw bytes landed before the last barrier: dequantise them into the other fp16 tile
+        auto convert = [&]() {
+            if constexpr (L::AHEAD >= 2) pf_convert<KVT>(s_raw[(i + 1) % L::NBUF], s_k[cur ^ 1], s_vt[cur ^ 1], t);
+        };
+
+        f4 sc[PF_RT][PF_KT];
+        h8 pb[PF_RT];
+        // ---- S^T = K Q^T for PF_KT key tiles of 16 (lane: key k0 + 16 k4 + 4 lg + i, row (rt, i16))
+        auto scores = [&]() {
 #pragma unroll
-    for (int rt = 0; rt < PF_RT; rt++) {
-        float lt = l[rt];
-        lt += __shfl_xor(lt, 16, 64);
-        lt += __shfl_xor(lt, 32, 64);
-        if (qpos[rt] < 0) continue;
-        const float il = 1.0f / lt;
-        const size_t base = ((size_t)tq[rt] * NH + g * GRP + hh[rt]) * HD;
+            for (int k4 = 0; k4 < PF_KT; k4++)
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++) {
-            const int d = 16 * dt + 4 * lg;
-            const float4 gv = *reinterpret_cast<const float4*>(gate + base + d);
-            const float gg[4] = {gv.x, gv.y, gv.z, gv.w};
-            uint16_t hv[4];
+                for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int i = 0; i < 4; i++) hv[i] = f2h_bits(o[rt][dt][i] * il * sigmoid(gg[i]));
-            *reinterpret_cast<uint2*>(out16 + base + d) =
-                make_uint2((uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16));
+            for (int s = 0; s < 8; s++) {
+#pragma unroll
+                for (int k4 = 0; k4 < PF_KT; k4++) {
+                    const h8 a = lds_h8(Ks + (16 * k4 + i16) * KS_LD + 8 * lg + 32 * s);
+#pragma unroll
+                    for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = mfma16(a, qb[rt][s], sc[rt][k4]);
+                }
+            }
+        };
+
+        // ---- mask + online softmax.  The reference maximum m moves only when a score exceeds it by more than
+        // PF_RESCALE_T (probabilities stay <= e^PF_RESCALE_T, far inside fp16), so the accumulators are rarely
+        // rescaled.
+        auto softmax = [&]() {
+            const bool need_mask = k0 + PF_TILE - 1 > wave_qmin;
+            float cr[PF_RT];
+#pragma unroll
+            for (int rt = 0; rt < PF_RT; rt++) {
+                if (need_mask) {
+#pragma unroll
+                    for (int k4 = 0; k4 < PF_KT; k4++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int key = k0 + 16 * k4 + 4 * lg + j;
+                            sc[rt][k4][j] = key > qpos[rt] ? -INFINITY : sc[rt][k4][j];
+                        }
+                }
+                float mx = -INFINITY;
+#pragma unroll
+                for (int k4 = 0; k4 < PF_KT; k4++)
+                    mx = max3f(max3f(mx, sc[rt][k4][0], sc[rt][k4][1]), sc[rt][k4][2], sc[rt][k4][3]);
+                mx = rows_max(mx);
+                const float mn = mx > m[rt] + PF_RESCALE_T ? mx : m[rt];
+                cr[rt] = mn == m[rt] ? 1.0f : fast_exp2((m[rt] - mn) * PF_LOG2E);  // m = -inf: c = 0
+                m[rt] = mn;
+                const float msl = mn == -INFINITY ? 0.0f : mn * PF_LOG2E;
+                float rs = 0.0f;
+                h8 p;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float e = fast_exp2(fmaf(sc[rt][j >> 2][j & 3], PF_LOG2E, -msl));
+                    rs += e;
+                    p[j] = (_Float16)e;
+                }
+                pb[rt] = p;
+                l[rt] = l[rt] * cr[rt] + rs;
+            }
+            if (__any(cr[0] != 1.0f || cr[PF_RT - 1] != 1.0f)) {
+#pragma unroll
+                for (int rt = 0; rt < PF_RT; rt++)
+#pragma unroll
+                    for (int dt = 0; dt < 16; dt++) o[rt][dt] *= cr[rt];
+            }
+        };
+
+        // ---- O^T += V^T P^T over 16 dim tiles; the fragment of dim tile dt + PF_VD - 1 is read while dt multiplies
+        auto pv = [&]() {
+            h8 vf[PF_VD];
+#pragma unroll
+            for (int dt = 0; dt < PF_VD - 1; dt++) vf[dt] = lds_h8(Vt + (16 * dt + i16) * VT_LD + 8 * lg);
+#pragma unroll
+            for (int dt = 0; dt < 16; dt++) {
+                if (dt + PF_VD - 1 < 16)
+                    vf[(dt + PF_VD - 1) % PF_VD] = lds_h8(Vt + (16 * (dt + PF_VD - 1) + i16) * VT_LD + 8 * lg);
+#pragma unroll
+                for (int rt = 0; rt < PF_RT; rt++) o[rt][dt] = mfma16(vf[dt % PF_VD], pb[rt], o[rt][dt]);
+            }
+        };
+
+        if (lead) convert();
+        scores();
+        softmax();
+        pv();
+        if (!lead) convert();
+
+        if constexpr (L::AHEAD >= 2) {
+            // tile i + 2 must have landed before the next iteration dequantises it; later tiles may stay in flight
+            wait_vm(nvm * (L::AHEAD - 2));
+            __syncthreads();
+        } else {
+            wait_vm(0);
+            __syncthreads();
+            if (i + 1 < nt) pf_convert<KVT>(s_raw[(i + 1) % L::NBUF], s_k[cur ^ 1], s_vt[cur ^ 1], t);
+            __syncthreads();
         }
     }
+    wait_vmcnt<0>();  // no direct-to-LDS load outlives the workgroup
+
+    // ---- partial state of this split: (m, l) and unnormalised O; lane holds dims 16 dt + 4 lg + i of row (rt, i16)
+#pragma unroll
+    for (int rt = 0; rt < PF_RT; rt++) {
+        const float lt = rows_sum(l[rt]);
+        if (qpos[rt] < 0) continue;
+        const int r = wrow0 + 16 * rt + i16, rr = (r / GRP) * NH + g * GRP + r % GRP;
+        const size_t prow = (size_t)sp * PF_MAXROWS + rr;
+        if (lg == 0) pf_part_ml[prow] = make_float2(m[rt], lt);
+        float4* dst = pf_part_o + prow * (HD / 4);
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++)
+            dst[4 * dt + lg] = make_float4(o[rt][dt][0], o[rt][dt][1], o[rt][dt][2], o[rt][dt][3]);
+    }
+}
+
+// Merges the PF_NS partial states of each output row in split order, normalises, applies the sigmoid gate and
+// writes fp16: one wave per row (token * NH + head), 4 dims per lane.
+__global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ gate, int nrows,
+                                                      uint16_t* __restrict__ out16) {
+    const int rr = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (rr >= nrows) return;
+    float2 ml[PF_NS];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < PF_NS; s++) {
+        ml[s] = pf_part_ml[(size_t)s * PF_MAXROWS + rr];
+        mx = fmaxf(mx, ml[s].x);
+    }
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float lsum = 0.0f;
+#pragma unroll
+    for (int s = 0; s < PF_NS; s++) {
+        // a split that saw no visible key has m = -inf, l = 0, O = 0: weight 0
+        const float w = ml[s].x == -INFINITY ? 0.0f : fast_exp2((ml[s].x - mx) * PF_LOG2E);
+        const float4 v = pf_part_o[((size_t)s * PF_MAXROWS + rr) * (HD / 4) + lane];
+        acc.x += w * v.x;
+        acc.y += w * v.y;
+        acc.z += w * v.z;
+        acc.w += w * v.w;
+        lsum += w * ml[s].y;
+    }
+    const float il = 1.0f / lsum;
+    const float4 gv = *reinterpret_cast<const float4*>(gate + (size_t)rr * HD + 4 * lane);
+    const uint16_t h0 = f2h_bits(acc.x * il * sigmoid(gv.x)), h1 = f2h_bits(acc.y * il * sigmoid(gv.y));
+    const uint16_t h2v = f2h_bits(acc.z * il * sigmoid(gv.z)), h3 = f2h_bits(acc.w * il * sigmoid(gv.w));
+    *reinterpret_cast<uint2*>(out16 + (size_t)rr * HD + 4 * lane) =
+        make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2v | ((uint32_t)h3 << 16));
 }
 
 hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
                           uint16_t* out16, hipStream_t st) {
-    const dim3 grid((GRP * B + PF_ROWS - 1) / PF_ROWS, NKV);
     profile_mark_begin(st);
-    if (kvt == QWA_KV_F16) hipLaunchKernelGGL(k_prefill<QWA_KV_F16>, grid, dim3(PF_THREADS), 0, st, q, gate, kv, B, p0, out16);
-    else if (kvt == QWA_KV_Q8_0) hipLaunchKernelGGL(k_prefill<QWA_KV_Q8_0>, grid, dim3(PF_THREADS), 0, st, q, gate, kv, B, p0, out16);
-    else hipLaunchKernelGGL(k_prefill<QWA_KV_Q4_0>, grid, dim3(PF_THREADS), 0, st, q, gate, kv, B, p0, out16);
+    for (int t0 = 0; t0 < B; t0 += PF_MAXB) {
+        const int nb = min(PF_MAXB, B - t0);
+        const float* qp = q + (size_t)t0 * NH * HD;
+        const dim3 grid((GRP * nb + PF_ROWS - 1) / PF_ROWS, NKV, PF_NS);
+        if (kvt == QWA_KV_F16)
+            hipLaunchKernelGGL(k_prefill<QWA_KV_F16>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0);
+        else if (kvt == QWA_KV_Q8_0)
+            hipLaunchKernelGGL(k_prefill<QWA_KV_Q8_0>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0);
+        else
+            hipLaunchKernelGGL(k_prefill<QWA_KV_Q4_0>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0);
+        const int nrows = nb * NH;
+        hipLaunchKernelGGL(k_pf_combine, dim3((nrows + 3) / 4), dim3(256), 0, st, gate + (size_t)t0 * NH * HD, nrows,
+                           out16 + (size_t)t0 * NH * HD);
+    }
     profile_mark_end(st);
     return hipGetLastError();
 }

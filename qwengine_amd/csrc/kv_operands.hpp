@@ -171,4 +171,42 @@ __device__ __forceinline__ void v_pair(const VRaw<KVT>& a, const VRaw<KVT>& b, u
 
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
+// ---- direct-to-LDS loads
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Direct-to-LDS loads written as inline asm: the compiler's wait-count pass would otherwise treat every later LDS
+// read as possibly reading the in-flight DMA data and wait for all outstanding loads (vmcnt(0)), which serialises the
+// chunk ring.  The kernel orders them itself: s_waitcnt vmcnt before reading a slot, lgkmcnt(0) before refilling it.
+// LDS destination = m0 + lane * size; source = scalar base + per-lane 32-bit offset (or a per-lane 64-bit address).
+// An SALU write of m0 needs one wait state before an LDS DMA reads it (the s_nop).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <int SIZE>
+__device__ __forceinline__ void dma_sv(uint32_t lds, const void* sbase, uint32_t voff) {
+    if constexpr (SIZE == 16)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
+    else if constexpr (SIZE == 4)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_ushort %1, %2" ::"s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
+}
+template <int SIZE>
+__device__ __forceinline__ void dma_v(uint32_t lds, const void* addr) {
+    if constexpr (SIZE == 16)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
+    else if constexpr (SIZE == 4)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_ushort %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+
 }  // namespace qwa
