@@ -30,11 +30,11 @@ namespace qwa {
 constexpr int PF_WAVES = QWA_PF_WAVES;           // MFMA waves per workgroup
 constexpr int PF_THREADS = PF_WAVES * 64;
 constexpr int PF_WPE = PF_WAVES / 4;             // waves per SIMD
-constexpr int PF_RT = 16 / PF_WAVES;             // 16-row MFMA tiles per wave
-constexpr int PF_ROWS = PF_WAVES * PF_RT * 16;   // 256 rows per workgroup
+constexpr int PF_RT = 16 / PF_WAVES > 0 ? 16 / PF_WAVES : 1;  // 16-row MFMA tiles per wave
+constexpr int PF_ROWS = PF_WAVES * PF_RT * 16;   // rows per workgroup
 constexpr int PF_TILE = 32;                      // keys per tile
 constexpr int PF_KT = PF_TILE / 16;              // 16-key MFMA tiles per tile
-constexpr int PF_NS = 8;                         // key-range splits per row block
+constexpr int PF_NS = PF_ROWS == 192 ? 6 : 8;    // key-range splits per row block (3 rounds of the chip for B = 1024)
 constexpr int PF_MAXB = 1024;                    // tokens per pass
 constexpr int PF_MAXROWS = PF_MAXB * NH;         // output rows per pass
 constexpr int KS_LD = HD + 8;                    // K tile row stride (halves)
@@ -209,11 +209,15 @@ __device__ __forceinline__ void pf_convert_kv(const uint8_t* raw, _Float16* Ks, 
     }
 }
 
-// 512 threads convert K and V; 1024 threads split them (threads 0-511 K, 512-1023 V)
+// The conversion is cut into 512 K units and 512 V units, spread over the workgroup's threads
 template <int KVT>
 __device__ __forceinline__ void pf_convert(const uint8_t* raw, _Float16* Ks, _Float16* Vt, int t) {
-    if constexpr (PF_THREADS == 512) pf_convert_kv<KVT>(raw, Ks, Vt, t, true, true);
-    else pf_convert_kv<KVT>(raw, Ks, Vt, t & 511, t < 512, t >= 512);
+    if constexpr (PF_THREADS == 512) {
+        pf_convert_kv<KVT>(raw, Ks, Vt, t, true, true);
+    } else {
+#pragma unroll
+        for (int u = t; u < 1024; u += PF_THREADS) pf_convert_kv<KVT>(raw, Ks, Vt, u & 511, u < 512, u >= 512);
+    }
 }
 
 __device__ __forceinline__ h8 lds_h8(const _Float16* p) { return *reinterpret_cast<const h8*>(p); }
