@@ -13,7 +13,8 @@
 //    Q / 16 as fp16 hi + lo parts, the key's fp16 block scale applied to each block's fp32 partial dot (scores exact
 //    up to fp32 accumulation, so outlier logits stay within tolerance); a lane then holds 4 keys of ONE row: the
 //    online softmax is lane-local up to a 4-lane max / sum, and P^T is directly the B operand of
-//    O^T += V^T P^T (v_mfma_f32_16x16x16_f16, V dequantized to fp16 in registers, fp32 accumulation);
+//    O^T += V^T P^T (v_mfma_f32_16x16x16_f16, fp32 accumulation; for Q4_0 the V operand holds the exact codes and
+//    the keys' block scales multiply the P operand, one product per block instead of one per V element);
 //  * the 4 classes of a workgroup are merged as fold(fold(c0, c1), fold(c2, c3)) into one partial record
 //    (m, l, O[256]) per row; k_dec_combine merges the records in a fixed order, normalises, applies the sigmoid gate
 //    and the optional ActQ8 epilogue.
@@ -141,9 +142,12 @@ __device__ __forceinline__ void fold(float& m, float& l, f4* o, float m2, float 
     const float M = fmaxf(m, m2);
     const float Ms = M == -INFINITY ? 0.0f : M;
     const float fa = fast_exp2((m - Ms) * LOG2E), fb = fast_exp2((m2 - Ms) * LOG2E);
-    l = l * fa + l2 * fb;
+    // explicit fused forms: every kernel that merges rounds the same way (the nq-independence contract)
+    l = fmaf(l, fa, l2 * fb);
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++) o[dt] = o[dt] * fa + o2[dt] * fb;
+    for (int dt = 0; dt < 16; dt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[dt][i] = fmaf(o[dt][i], fa, o2[dt][i] * fb);
     m = M;
 }
 
@@ -502,6 +506,20 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;
     const size_t rowbase = (size_t)g * kv.capacity;
 
+    uint8_t(*ring)[Q4Chunk::BYTES] = s_u.ring[wave];
+    const Q4Offsets off = q4_offsets(lane);
+    auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * j); };
+    auto issue = [&](int j) {
+        const int kb = chunk_key(j);
+        const uint32_t dst = lds_addr(ring[j % NST]);
+        if (kb + CHUNK - 1 <= kmax) q4_issue_full(dst, kv, rowbase + kb, off, lane);
+        else q4_issue_tail(dst, kv, rowbase, kb, kmax, lane);
+    };
+    // the first chunks' loads go out before the Q set-up, so their latency overlaps it
+#pragma unroll
+    for (int st = 0; st < NST; st++)
+        if (st < nmine) issue(st);
+
     // Q / 16 as fp16 hi + lo, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + k_perm(j)
     h8 qh[8], ql[8];
     const int r = 16 * rt0 + i16;
@@ -530,17 +548,8 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
     float mthr = -INFINITY;  // m + RESCALE_T
 
     if (nmine > 0) {
-        uint8_t(*ring)[Q4Chunk::BYTES] = s_u.ring[wave];
-        const Q4Offsets off = q4_offsets(lane);
         const Q4Masks km = q4_masks();
         const uint32_t bsel = (uint32_t)(i16 & 3) | 0x0c000c00u | ((uint32_t)(4 + (i16 & 3)) << 16);
-        auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * j); };
-        auto issue = [&](int j) {
-            const int kb = chunk_key(j);
-            const uint32_t dst = lds_addr(ring[j % NST]);
-            if (kb + CHUNK - 1 <= kmax) q4_issue_full(dst, kv, rowbase + kb, off, lane);
-            else q4_issue_tail(dst, kv, rowbase, kb, kmax, lane);
-        };
         // K of chunk j from LDS: the 8 code dwords of this lane and the block scales of its 4 keys
         struct KRegs {
             uint32_t w[8];
@@ -625,23 +634,24 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
         // (dim pair i16, group lg) holds keys in the order {4 lg, 4 lg + 2, 4 lg + 1, 4 lg + 3}
         auto pv = [&](const VRegs& r, h4 P) {
             const h2 b_lo = {(_Float16)1032.0f, (_Float16)1032.0f}, b_hi = {(_Float16)72.0f, (_Float16)72.0f};
+            const uint32_t P02 = __builtin_bit_cast(uint2, P).x, P13 = __builtin_bit_cast(uint2, P).y;
 #pragma unroll
             for (int b = 0; b < 8; b++) {
                 const uint32_t sel = (b & 1) ? 0x07060302u : 0x05040100u;  // halfword b & 1 of both words
                 const h2 d02 = bits_h2(__builtin_amdgcn_perm(r.d[2][b >> 1], r.d[0][b >> 1], sel));
                 const h2 d13 = bits_h2(__builtin_amdgcn_perm(r.d[3][b >> 1], r.d[1][b >> 1], sel));
-                const uint32_t e02 = h2_bits((bits_h2((r.x02[b] & km.lo) | km.e_lo) - b_lo) * d02);
-                const uint32_t e13 = h2_bits((bits_h2((r.x13[b] & km.lo) | km.e_lo) - b_lo) * d13);
-                const uint32_t f02 = h2_bits((bits_h2((r.x02[b] & km.hi) | km.e_hi) - b_hi) * d02);
-                const uint32_t f13 = h2_bits((bits_h2((r.x13[b] & km.hi) | km.e_hi) - b_hi) * d13);
-                o[2 * b] = mfma16k16(make_h4(e02, e13), P, o[2 * b]);
-                o[2 * b + 1] = mfma16k16(make_h4(f02, f13), P, o[2 * b + 1]);
+                // the V operand holds the exact codes; the keys' block scales multiply the P operand instead (the
+                // lane's P keys are the keys of its V operand)
+                const h4 Pb = make_h4(h2_bits(bits_h2(P02) * d02), h2_bits(bits_h2(P13) * d13));
+                const uint32_t e02 = h2_bits(bits_h2((r.x02[b] & km.lo) | km.e_lo) - b_lo);
+                const uint32_t e13 = h2_bits(bits_h2((r.x13[b] & km.lo) | km.e_lo) - b_lo);
+                const uint32_t f02 = h2_bits(bits_h2((r.x02[b] & km.hi) | km.e_hi) - b_hi);
+                const uint32_t f13 = h2_bits(bits_h2((r.x13[b] & km.hi) | km.e_hi) - b_hi);
+                o[2 * b] = mfma16k16(make_h4(e02, e13), Pb, o[2 * b]);
+                o[2 * b + 1] = mfma16k16(make_h4(f02, f13), Pb, o[2 * b + 1]);
             }
         };
 
-#pragma unroll
-        for (int st = 0; st < NST; st++)
-            if (st < nmine) issue(st);
         for (int j = 0; j < nmine; j++) {
             if (j + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
             else wait_vmcnt<0>();
