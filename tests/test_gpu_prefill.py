@@ -1,7 +1,8 @@
 """GPU parity of causal prefill attention (fp16 MFMA kernel) against the float64 oracle on the stored cache, and
 against the FP32 test kernel at the reference's chunk cases (tests/kernels/test_attn_prefill.cu:20-72: a cache of
 1500 positions filled through rope_table + attn_prep_rows, chunks (p0, B) in {(0,37), (0,512), (300,129),
-(1000,500), (1480,20)}), plus the BASELINE 1024-token chunk at p0 = 32768 on a sample of its queries."""
+(1000,500), (1480,20)}), plus a 1300-token chunk (two passes of the kernel's 1024-token limit) and the BASELINE
+1024-token chunk at p0 = 32768 on a sample of its queries."""
 import numpy as np
 import pytest
 import torch
@@ -11,7 +12,7 @@ from kvutil import KVTS, KV_NAMES, assert_close, dequant_cache, make_cache, seed
 
 pytestmark = pytest.mark.gpu
 
-CASES = [(0, 37), (0, 512), (300, 129), (1000, 500), (1480, 20)]
+CASES = [(0, 37), (0, 512), (300, 129), (1000, 500), (1480, 20), (200, 1300)]
 
 
 @pytest.fixture(scope="module", params=KVTS, ids=lambda k: KV_NAMES[k])
