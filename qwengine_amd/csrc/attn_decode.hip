@@ -515,10 +515,9 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
         if (kb + CHUNK - 1 <= kmax) q4_issue_full(dst, kv, rowbase + kb, off, lane);
         else q4_issue_tail(dst, kv, rowbase, kb, kmax, lane);
     };
-    // the first chunks' loads go out before the Q set-up, so their latency overlaps it
-#pragma unroll
-    for (int st = 0; st < NST; st++)
-        if (st < nmine) issue(st);
+    // the first chunk's loads go out before the Q set-up, so their latency overlaps it (the Q loads complete after
+    // them); the rest of the ring follows the set-up, so the first iteration waits for chunk 0 only
+    if (nmine > 0) issue(0);
 
     // Q / 16 as fp16 hi + lo, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + k_perm(j)
     h8 qh[8], ql[8];
@@ -548,6 +547,9 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
     float mthr = -INFINITY;  // m + RESCALE_T
 
     if (nmine > 0) {
+#pragma unroll
+        for (int st = 1; st < NST; st++)
+            if (st < nmine) issue(st);
         const Q4Masks km = q4_masks();
         const uint32_t bsel = (uint32_t)(i16 & 3) | 0x0c000c00u | ((uint32_t)(4 + (i16 & 3)) << 16);
         // K of chunk j from LDS: the 8 code dwords of this lane and the block scales of its 4 keys
