@@ -489,13 +489,18 @@ __device__ __forceinline__ h8 q4_codes(uint32_t w, const Q4Masks& k) {
     return make_h8(e04, e15, e26, e37);
 }
 
-template <int NST>
+// RT row tiles per wave.  RT = 1 keeps Q in registers; RT = 2 (verify) keeps the Q fragments of both tiles in LDS
+// (shared by the 4 waves), so each chunk's K codes and V operands are unpacked once for both tiles while the wave
+// still fits two per SIMD.  A row's arithmetic is the same whatever RT is.
+template <int NST, int RT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work) {
+    constexpr bool QLDS = RT > 1;
     __shared__ __attribute__((aligned(16))) union {
         uint8_t ring[WG_CLASSES][NST][Q4Chunk::BYTES];
         MergeLds merge;
     } s_u;
+    __shared__ __attribute__((aligned(16))) h8 s_q[QLDS ? RT * 8 * 2 * 64 : 1];  // [rt][block][hi, lo][lane]
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
@@ -520,31 +525,49 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
     if (nmine > 0) issue(0);
 
     // Q / 16 as fp16 hi + lo, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + k_perm(j)
-    h8 qh[8], ql[8];
-    const int r = 16 * rt0 + i16;
-    const int qt = r / GRP, hh = r % GRP;
-    const int qpos = qt < nq ? pos0 + qt : -1;  // last visible key of this lane's row (-1: padding row)
-    {
-        const float* src = q + ((size_t)(qt < nq ? qt : 0) * NH + g * GRP + hh) * HD + 8 * lg;
+    h8 qh[QLDS ? 1 : RT][8], ql[QLDS ? 1 : RT][8];
+    int qt[RT], hh[RT], qpos[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int r = 16 * (rt0 + rt) + i16;
+        qt[rt] = r / GRP;
+        hh[rt] = r % GRP;
+        qpos[rt] = qt[rt] < nq ? pos0 + qt[rt] : -1;  // last visible key of this lane's row (-1: padding row)
+        if (QLDS && wave != rt) continue;  // with Q in LDS, wave rt fills tile rt's fragments
+        const float* src = q + ((size_t)(qt[rt] < nq ? qt[rt] : 0) * NH + g * GRP + hh[rt]) * HD + 8 * lg;
 #pragma unroll
         for (int b = 0; b < 8; b++) {
             const float4 a = *reinterpret_cast<const float4*>(src + 32 * b);
             const float4 c = *reinterpret_cast<const float4*>(src + 32 * b + 4);
             const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            h8 hi, lo;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const float v = qt < nq ? x[k_perm<QWA_KV_Q4_0>(j)] * 0.0625f : 0.0f;
-                qh[b][j] = (_Float16)v;
-                ql[b][j] = (_Float16)(v - (float)qh[b][j]);
+                const float v = qt[rt] < nq ? x[k_perm<QWA_KV_Q4_0>(j)] * 0.0625f : 0.0f;
+                hi[j] = (_Float16)v;
+                lo[j] = (_Float16)(v - (float)hi[j]);
+            }
+            if constexpr (QLDS) {
+                s_q[((rt * 8 + b) * 2 + 0) * 64 + lane] = hi;
+                s_q[((rt * 8 + b) * 2 + 1) * 64 + lane] = lo;
+            } else {
+                qh[QLDS ? 0 : rt][b] = hi;
+                ql[QLDS ? 0 : rt][b] = lo;
             }
         }
     }
-    f4 o[16];
+    if constexpr (QLDS) __syncthreads();
+    f4 o[RT][16];
+    float m[RT], l[RT], msl[RT], mthr[RT];  // msl = m * log2(e) (0 while m = -inf), mthr = m + RESCALE_T
 #pragma unroll
-    for (int t = 0; t < 16; t++) o[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m = -INFINITY, l = 0.0f;
-    float msl = 0.0f;        // m * log2(e), 0 while m = -inf
-    float mthr = -INFINITY;  // m + RESCALE_T
+    for (int rt = 0; rt < RT; rt++) {
+#pragma unroll
+        for (int t = 0; t < 16; t++) o[rt][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        m[rt] = -INFINITY;
+        l[rt] = 0.0f;
+        msl[rt] = 0.0f;
+        mthr[rt] = -INFINITY;
+    }
 
     if (nmine > 0) {
 #pragma unroll
@@ -589,54 +612,60 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
                 r.d[i][0] = u.x; r.d[i][1] = u.y; r.d[i][2] = u.z; r.d[i][3] = u.w;
             }
         };
-        // S^T of one chunk: per block the exact integer codes times Q_hi + Q_lo, times the key's block scale
-        auto scores = [&](const KRegs& r) {
-            f4 S = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        // S^T of one chunk for every row tile: per block the exact integer codes (unpacked once) times Q_hi + Q_lo,
+        // times the key's block scale
+        auto scores = [&](const KRegs& r, f4* S) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) S[rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int b = 0; b < 8; b++) {
                 const h8 ka = q4_codes(r.w[b], km);
-                f4 a = mfma16(ka, qh[b], f4{0.0f, 0.0f, 0.0f, 0.0f});
-                a = mfma16(ka, ql[b], a);
 #pragma unroll
-                for (int i = 0; i < 4; i++) S[i] = fmaf(h2f_bits((uint16_t)(r.d[i][b >> 1] >> (16 * (b & 1)))), a[i], S[i]);
+                for (int rt = 0; rt < RT; rt++) {
+                    const h8 bh = QLDS ? s_q[((rt * 8 + b) * 2 + 0) * 64 + lane] : qh[QLDS ? 0 : rt][b];
+                    const h8 bl = QLDS ? s_q[((rt * 8 + b) * 2 + 1) * 64 + lane] : ql[QLDS ? 0 : rt][b];
+                    f4 a = mfma16(ka, bh, f4{0.0f, 0.0f, 0.0f, 0.0f});
+                    a = mfma16(ka, bl, a);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        S[rt][i] = fmaf(h2f_bits((uint16_t)(r.d[i][b >> 1] >> (16 * (b & 1)))), a[i], S[rt][i]);
+                }
             }
-            return S;
         };
         // online softmax of chunk j (lane: keys kb + 4 lg + i of row i16) -> P^T operand, keys {0, 2}, {1, 3}
-        auto softmax = [&](int j, f4 S) {
+        auto softmax = [&](int j, f4 S, int rt) {
             const int kb = chunk_key(j);
             float sv[4] = {S[0], S[1], S[2], S[3]};
             if (kb + CHUNK - 1 > pos0) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) sv[i] = kb + 4 * lg + i <= qpos ? sv[i] : -INFINITY;
+                for (int i = 0; i < 4; i++) sv[i] = kb + 4 * lg + i <= qpos[rt] ? sv[i] : -INFINITY;
             }
             const float mx4 = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-            if (__any(mx4 > mthr)) {
+            if (__any(mx4 > mthr[rt])) {
                 const float mx = row_max4(mx4);
-                const float mn = mx > mthr ? mx : m;
-                const float cr = mn == m ? 1.0f : fast_exp2((m - mn) * LOG2E);  // m = -inf: cr = 0
+                const float mn = mx > mthr[rt] ? mx : m[rt];
+                const float cr = mn == m[rt] ? 1.0f : fast_exp2((m[rt] - mn) * LOG2E);  // m = -inf: cr = 0
                 if (__any(cr != 1.0f)) {
 #pragma unroll
-                    for (int t = 0; t < 16; t++) o[t] *= cr;
-                    l *= cr;
+                    for (int t = 0; t < 16; t++) o[rt][t] *= cr;
+                    l[rt] *= cr;
                 }
-                m = mn;
-                msl = mn == -INFINITY ? 0.0f : mn * LOG2E;
-                mthr = mn + RESCALE_T;
+                m[rt] = mn;
+                msl[rt] = mn == -INFINITY ? 0.0f : mn * LOG2E;
+                mthr[rt] = mn + RESCALE_T;
             }
             float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) p[i] = fast_exp2(fmaf(sv[i], LOG2E, -msl));
+            for (int i = 0; i < 4; i++) p[i] = fast_exp2(fmaf(sv[i], LOG2E, -msl[rt]));
             const h2 p02 = {(_Float16)p[0], (_Float16)p[2]}, p13 = {(_Float16)p[1], (_Float16)p[3]};
             const h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
-            l = __builtin_amdgcn_fdot2(p13, one2, __builtin_amdgcn_fdot2(p02, one2, l, false), false);
+            l[rt] = __builtin_amdgcn_fdot2(p13, one2, __builtin_amdgcn_fdot2(p02, one2, l[rt], false), false);
             return make_h4(h2_bits(p02), h2_bits(p13));
         };
         // O^T += V^T P^T: block b as two 16-dim tiles, even dims (tile 2 b) and odd dims (tile 2 b + 1); the lane
         // (dim pair i16, group lg) holds keys in the order {4 lg, 4 lg + 2, 4 lg + 1, 4 lg + 3}
-        auto pv = [&](const VRegs& r, h4 P) {
+        auto pv = [&](const VRegs& r, const h4* P) {
             const h2 b_lo = {(_Float16)1032.0f, (_Float16)1032.0f}, b_hi = {(_Float16)72.0f, (_Float16)72.0f};
-            const uint32_t P02 = __builtin_bit_cast(uint2, P).x, P13 = __builtin_bit_cast(uint2, P).y;
 #pragma unroll
             for (int b = 0; b < 8; b++) {
                 const uint32_t sel = (b & 1) ? 0x07060302u : 0x05040100u;  // halfword b & 1 of both words
@@ -644,46 +673,75 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
                 const h2 d13 = bits_h2(__builtin_amdgcn_perm(r.d[3][b >> 1], r.d[1][b >> 1], sel));
                 // the V operand holds the exact codes; the keys' block scales multiply the P operand instead (the
                 // lane's P keys are the keys of its V operand)
-                const h4 Pb = make_h4(h2_bits(bits_h2(P02) * d02), h2_bits(bits_h2(P13) * d13));
                 const uint32_t e02 = h2_bits(bits_h2((r.x02[b] & km.lo) | km.e_lo) - b_lo);
                 const uint32_t e13 = h2_bits(bits_h2((r.x13[b] & km.lo) | km.e_lo) - b_lo);
                 const uint32_t f02 = h2_bits(bits_h2((r.x02[b] & km.hi) | km.e_hi) - b_hi);
                 const uint32_t f13 = h2_bits(bits_h2((r.x13[b] & km.hi) | km.e_hi) - b_hi);
-                o[2 * b] = mfma16k16(make_h4(e02, e13), Pb, o[2 * b]);
-                o[2 * b + 1] = mfma16k16(make_h4(f02, f13), Pb, o[2 * b + 1]);
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++) {
+                    const uint2 pw = __builtin_bit_cast(uint2, P[rt]);
+                    const h4 Pb = make_h4(h2_bits(bits_h2(pw.x) * d02), h2_bits(bits_h2(pw.y) * d13));
+                    o[rt][2 * b] = mfma16k16(make_h4(e02, e13), Pb, o[rt][2 * b]);
+                    o[rt][2 * b + 1] = mfma16k16(make_h4(f02, f13), Pb, o[rt][2 * b + 1]);
+                }
             }
         };
 
         for (int j = 0; j < nmine; j++) {
             if (j + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
             else wait_vmcnt<0>();
-            KRegs kr;
-            read_k(j, kr);
-            VRegs vr;
-            read_v(j, vr);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot j is read out: refill it
-            if (j + NST < nmine) issue(j + NST);
-            const h4 P = softmax(j, scores(kr));
-            pv(vr, P);
+            if constexpr (RT == 1) {
+                KRegs kr;
+                read_k(j, kr);
+                VRegs vr;
+                read_v(j, vr);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot j is read out: refill it
+                if (j + NST < nmine) issue(j + NST);
+                f4 S[RT];
+                scores(kr, S);
+                h4 P[RT];
+                P[0] = softmax(j, S[0], 0);
+                pv(vr, P);
+            } else {
+                // two row tiles: V is read after the softmax, so K and V registers are never live together
+                f4 S[RT];
+                {
+                    KRegs kr;
+                    read_k(j, kr);
+                    scores(kr, S);
+                }
+                h4 P[RT];
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++) P[rt] = softmax(j, S[rt], rt);
+                VRegs vr;
+                read_v(j, vr);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot j is read out: refill it
+                if (j + NST < nmine) issue(j + NST);
+                pv(vr, P);
+            }
         }
     }
 
-    // ---- merge the 4 classes; wave 0 writes the records.  Lane (row i16, lg), tile 2 b + par, element i holds
-    // dim 32 b + 8 lg + 2 i + par.
-    if (merge4(s_u.merge, wave, lane, m, l, o)) {
-        const float lt = half4_sum(l);
-        if (qpos >= 0) {
-            float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt) * GRP + hh) * REC;
-            if (lg == 0) {
-                recp[0] = m;
-                recp[1] = lt;
-            }
+    // ---- merge the 4 classes of each row tile; wave 0 writes the records.  Lane (row i16, lg), tile 2 b + par,
+    // element i holds dim 32 b + 8 lg + 2 i + par.
 #pragma unroll
-            for (int b = 0; b < 8; b++) {
-                float* dst = recp + 4 + 32 * b + 8 * lg;
-                *reinterpret_cast<float4*>(dst) = make_float4(o[2 * b][0], o[2 * b + 1][0], o[2 * b][1], o[2 * b + 1][1]);
-                *reinterpret_cast<float4*>(dst + 4) =
-                    make_float4(o[2 * b][2], o[2 * b + 1][2], o[2 * b][3], o[2 * b + 1][3]);
+    for (int rt = 0; rt < RT; rt++) {
+        if (merge4(s_u.merge, wave, lane, m[rt], l[rt], o[rt])) {
+            const float lt = half4_sum(l[rt]);
+            if (qpos[rt] >= 0) {
+                float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt[rt]) * GRP + hh[rt]) * REC;
+                if (lg == 0) {
+                    recp[0] = m[rt];
+                    recp[1] = lt;
+                }
+#pragma unroll
+                for (int b = 0; b < 8; b++) {
+                    float* dst = recp + 4 + 32 * b + 8 * lg;
+                    *reinterpret_cast<float4*>(dst) =
+                        make_float4(o[rt][2 * b][0], o[rt][2 * b + 1][0], o[rt][2 * b][1], o[rt][2 * b + 1][1]);
+                    *reinterpret_cast<float4*>(dst + 4) =
+                        make_float4(o[rt][2 * b][2], o[rt][2 * b + 1][2], o[rt][2 * b][3], o[rt][2 * b + 1][3]);
+                }
             }
         }
     }
@@ -786,10 +844,17 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
     const int rt = (GRP * nq + 15) / 16;
     const dim3 grid(nrec, NKV);
     for (int t = 0; t < rt; t++) {
-        if constexpr (KVT == QWA_KV_Q4_0)
-            hipLaunchKernelGGL((k_dec4<3>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
-        else
+        if constexpr (KVT == QWA_KV_Q4_0) {
+            // two row tiles share one pass over the cache; a third tile gets a pass of its own
+            if (t + 1 < rt) {
+                hipLaunchKernelGGL((k_dec4<2, 2>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
+                t++;
+            } else {
+                hipLaunchKernelGGL((k_dec4<3, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
+            }
+        } else {
             hipLaunchKernelGGL((k_dec<KVT, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
+        }
     }
 }
 
