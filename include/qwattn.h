@@ -121,6 +121,17 @@ int qwa_attn_prefill_simple(const float* q, const float* gate, const qwa_kv_laye
  * (src/cuda/common.cuh:199-228), exposed on its own so callers holding already-roped K can append them. */
 int qwa_kv_append(const float* xk, const float* xv, int pos0, int n, int kvt, const qwa_kv_layer* kv, void* stream);
 
+/* KV-cache lifecycle (no operator counterpart: the engine's resize, src/runtime/engine.cpp:248-275, parks "only the
+ * P positions in use, per KV head" in host memory with per-head cudaMemcpy calls and restores them into a layer of
+ * the new capacity; these calls do that move with the same packed layout).
+ * The packed layout is the engine's park layout: K values [4][n_pos][vb], V values [4][n_pos][vb], then for Q8_0 /
+ * Q4_0 K scales [4][n_pos][16 B] and V scales [4][n_pos][16 B]; qwa_kv_packed_bytes gives its size.  dst / src may
+ * be device memory or pinned host memory (hipHostMalloc); the copies are stream-ordered pitched DMA transfers.
+ * n_pos must fit the layer's capacity. */
+long long qwa_kv_packed_bytes(int kvt, int n_pos);
+int qwa_kv_pack(const qwa_kv_layer* kv, int kvt, int n_pos, void* dst, void* stream);
+int qwa_kv_unpack(const void* src, const qwa_kv_layer* kv, int kvt, int n_pos, void* stream);
+
 /* Opt-in kernel timing (no reference counterpart; the reference times phases with env-gated GPU timers,
  * src/runtime/engine.cpp:2477-2480): between qwa_profile_begin() and qwa_profile_end(), every attention call records
  * HIP events around its main kernel (decode: the split-K kernel; prefill: the MFMA kernel).  qwa_profile_end()

@@ -218,6 +218,51 @@ int qwa_kv_append(const float* xk, const float* xv, int pos0, int n, int kvt, co
     return from_hip(qwa::launch_kv_append(xk, xv, pos0, n, kvt, *kv, as_stream(stream)), fn);
 }
 
+long long qwa_kv_packed_bytes(int kvt, int n_pos) {
+    if (!kvt_ok(kvt) || n_pos < 0) return -1;
+    return (long long)qwa::NKV * n_pos * 2 * (long long)(qwa_kv_value_bytes(kvt) + qwa_kv_scale_bytes(kvt));
+}
+
+namespace {
+// one pitched copy per buffer: 4 rows (KV heads) of n_pos * row bytes, at pitch capacity * row bytes in the layer
+// and n_pos * row bytes in the packed buffer
+int kv_move(const qwa_kv_layer* kv, int kvt, int n_pos, uint8_t* packed, bool to_packed, void* stream,
+            const char* fn) {
+    int st;
+    if ((st = check_kv(kv, kvt, fn))) return st;
+    if (!packed) return fail(QWA_ERR_INVALID, "%s: null packed buffer", fn);
+    if (n_pos < 0 || n_pos > kv->capacity)
+        return fail(QWA_ERR_RANGE, "%s: %d positions do not fit the capacity %d", fn, n_pos, kv->capacity);
+    if (n_pos == 0) return QWA_OK;
+    const size_t vb = qwa_kv_value_bytes(kvt), sb = qwa_kv_scale_bytes(kvt), P = (size_t)n_pos;
+    const size_t cap = (size_t)kv->capacity;
+    uint8_t* bufs[4] = {kv->k, kv->v, reinterpret_cast<uint8_t*>(kv->ks), reinterpret_cast<uint8_t*>(kv->vs)};
+    const size_t row[4] = {vb, vb, sb, sb};
+    size_t off = 0;
+    for (int i = 0; i < (sb ? 4 : 2); i++) {
+        const size_t w = P * row[i];
+        hipError_t e;
+        if (to_packed)
+            e = hipMemcpy2DAsync(packed + off, w, bufs[i], cap * row[i], w, qwa::NKV, hipMemcpyDefault,
+                                 as_stream(stream));
+        else
+            e = hipMemcpy2DAsync(bufs[i], cap * row[i], packed + off, w, w, qwa::NKV, hipMemcpyDefault,
+                                 as_stream(stream));
+        if (e != hipSuccess) return from_hip(e, fn);
+        off += (size_t)qwa::NKV * w;
+    }
+    return QWA_OK;
+}
+}  // namespace
+
+int qwa_kv_pack(const qwa_kv_layer* kv, int kvt, int n_pos, void* dst, void* stream) {
+    return kv_move(kv, kvt, n_pos, static_cast<uint8_t*>(dst), true, stream, "kv_pack");
+}
+
+int qwa_kv_unpack(const void* src, const qwa_kv_layer* kv, int kvt, int n_pos, void* stream) {
+    return kv_move(kv, kvt, n_pos, static_cast<uint8_t*>(const_cast<void*>(src)), false, stream, "kv_unpack");
+}
+
 int qwa_profile_begin(void) {
     g_prof.on = true;
     g_prof.n = 0;

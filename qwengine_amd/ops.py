@@ -73,6 +73,11 @@ EXPORTS = {
                                 [ctypes.c_int] * 3 + [ctypes.c_void_p] * 2),
     "qwa_kv_append": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.c_int] * 3 + [ctypes.POINTER(_KVLayerC),
                                                                                   ctypes.c_void_p]),
+    "qwa_kv_packed_bytes": (ctypes.c_longlong, [ctypes.c_int, ctypes.c_int]),
+    "qwa_kv_pack": (ctypes.c_int, [ctypes.POINTER(_KVLayerC), ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_void_p]),
+    "qwa_kv_unpack": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(_KVLayerC), ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_void_p]),
     "qwa_profile_begin": (ctypes.c_int, []),
     "qwa_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
     "qwa_status_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -294,6 +299,21 @@ def profile_end() -> tuple[float, int]:
     n = ctypes.c_int(0)
     _check(lib().qwa_profile_end(ctypes.byref(ms), ctypes.byref(n)))
     return ms.value, n.value
+
+
+def kv_packed_bytes(kvt, n_pos: int) -> int:
+    """Bytes of the packed (parked) form of the first n_pos positions of a layer (the engine's resize layout)."""
+    return int(lib().qwa_kv_packed_bytes(_kvt(kvt), n_pos))
+
+
+def kv_pack(kv: KVLayer, kvt, n_pos: int, dst, stream=None) -> None:
+    """Copies positions [0, n_pos) of every KV head into dst (device tensor or pinned host tensor), packed."""
+    _check(lib().qwa_kv_pack(ctypes.byref(kv.c()), _kvt(kvt), n_pos, _ptr(dst), _stream(stream)))
+
+
+def kv_unpack(src, kv: KVLayer, kvt, n_pos: int, stream=None) -> None:
+    """Restores a packed prefix into positions [0, n_pos) of a layer of any capacity >= n_pos."""
+    _check(lib().qwa_kv_unpack(_ptr(src), ctypes.byref(kv.c()), _kvt(kvt), n_pos, _stream(stream)))
 
 
 def kv_append(xk, xv, pos0: int, n: int, kvt, kv: KVLayer, stream=None) -> None:

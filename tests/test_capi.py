@@ -81,6 +81,18 @@ def test_rejects_bad_kv():
         ops.attn_prefill(0x1000, 0x1000, _kv("f16", 100), "f16", 0, 0, 0x1000)
 
 
+def test_kv_lifecycle_sizes_and_validation():
+    # packed bytes: 4 heads x n positions x (K + V) x (values + scales)
+    assert ops.kv_packed_bytes("f16", 10) == 4 * 10 * 2 * 512
+    assert ops.kv_packed_bytes("q8_0", 10) == 4 * 10 * 2 * (256 + 16)
+    assert ops.kv_packed_bytes("q4_0", 150000) == 150000 * 1152
+    with pytest.raises(ops.QwaError, match="do not fit"):
+        ops.kv_pack(_kv("q4_0", 100), "q4_0", 101, 0x1000)
+    with pytest.raises(ops.QwaError, match="null packed buffer"):
+        ops.kv_unpack(0, _kv("q8_0", 100), "q8_0", 10)
+    ops.kv_pack(_kv("q8_0", 100), "q8_0", 0, 0x1000)  # nothing to move: returns before any copy
+
+
 def test_prep_rejects_bad_row_sources():
     kv = _kv("q4_0")
     src = ops.RowSrc(0x1000, 12288)
