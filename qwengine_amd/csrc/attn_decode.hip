@@ -138,6 +138,7 @@ __device__ __forceinline__ float row_max4(float x) {
 __device__ __forceinline__ f4 mfma16k16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
 // Merge of two partial softmax states (fold step); the same arithmetic for every record and every nq.
+template <int NT = 16>
 __device__ __forceinline__ void fold(float& m, float& l, f4* o, float m2, float l2, const f4* o2) {
     const float M = fmaxf(m, m2);
     const float Ms = M == -INFINITY ? 0.0f : M;
@@ -145,7 +146,7 @@ __device__ __forceinline__ void fold(float& m, float& l, f4* o, float m2, float 
     // explicit fused forms: every kernel that merges rounds the same way (the nq-independence contract)
     l = fmaf(l, fa, l2 * fb);
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++)
+    for (int dt = 0; dt < NT; dt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) o[dt][i] = fmaf(o[dt][i], fa, o2[dt][i] * fb);
     m = M;
@@ -196,6 +197,39 @@ __device__ __forceinline__ float half4_sum(float x) {
     return x + __shfl_xor(x, 32, 64);
 }
 
+// Q / 16 as fp16 hi + lo MFMA B-operand fragments of RT row tiles, written to LDS by the whole workgroup:
+// s_q[((rt * 8 + b) * 2 + part) * 64 + lane] holds, for lane (row i16, group lg) of tile rt0 + rt, the dims
+// 32 b + 8 lg + k_perm(j) (part 0: hi = fp16(Q / 16), part 1: lo = fp16(Q / 16 - hi)); padding rows are zero.
+// Every fragment is loaded once per workgroup: loading the rows per wave sends several times the bytes through the
+// few L2 channels that hold Q, and at kernel start that load sits on every wave's critical path.  The caller
+// synchronises the workgroup before reading the fragments.
+template <int KVT, int RT>
+__device__ __forceinline__ void q_frags_to_lds(const float* __restrict__ q, int nq, int g, int rt0, h8* s_q) {
+    for (int f = threadIdx.x; f < RT * 8 * 64; f += blockDim.x) {
+        const int rt = f >> 9, b = (f >> 6) & 7, ln = f & 63;
+        const int r = 16 * (rt0 + rt) + (ln & 15);
+        const int qt = r / GRP, hh = r % GRP;
+        h8 hi, lo;
+        if (qt < nq) {
+            const float* src = q + ((size_t)qt * NH + g * GRP + hh) * HD + 32 * b + 8 * (ln >> 4);
+            const float4 a = *reinterpret_cast<const float4*>(src);
+            const float4 c = *reinterpret_cast<const float4*>(src + 4);
+            const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float v = x[k_perm<KVT>(j)] * 0.0625f;
+                hi[j] = (_Float16)v;
+                lo[j] = (_Float16)(v - (float)hi[j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) hi[j] = lo[j] = (_Float16)0.0f;
+        }
+        s_q[((rt * 8 + b) * 2 + 0) * 64 + ln] = hi;
+        s_q[((rt * 8 + b) * 2 + 1) * 64 + ln] = lo;
+    }
+}
+
 // ring depth (chunks in flight per wave): sized so that two 4-wave workgroups fit a CU's 160 KB of LDS where possible
 template <int KVT, int RT> struct DecCfg {
     static constexpr int NST = KVT == QWA_KV_Q4_0 ? (RT == 1 ? 3 : 2) : 1;
@@ -222,27 +256,19 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;  // chunks of this wave
     const size_t rowbase = (size_t)g * kv.capacity;
 
-    // Q / 16 as fp16 hi + lo parts, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + perm(j)
+    // Q / 16 as fp16 hi + lo parts, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + perm(j);
+    // the fragments are loaded once per workgroup through LDS
+    __shared__ __attribute__((aligned(16))) h8 s_q[RT * 8 * 2 * 64];
+    q_frags_to_lds<KVT, RT>(q, nq, g, rt0, s_q);
+    __syncthreads();
     h8 qh[RT][8], ql[RT][8];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-        const int r = 16 * (rt0 + rt) + i16;
-        const int qt = r / GRP, hh = r % GRP;
-        const bool valid = qt < nq;
-        const float* src = q + ((size_t)(valid ? qt : 0) * NH + g * GRP + hh) * HD + 8 * lg;
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int b = 0; b < 8; b++) {
-            const float4 a = *reinterpret_cast<const float4*>(src + 32 * b);
-            const float4 c = *reinterpret_cast<const float4*>(src + 32 * b + 4);
-            const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float v = valid ? x[k_perm<KVT>(j)] * 0.0625f : 0.0f;
-                qh[rt][b][j] = (_Float16)v;
-                ql[rt][b][j] = (_Float16)(v - (float)qh[rt][b][j]);
-            }
+            qh[rt][b] = s_q[((rt * 8 + b) * 2 + 0) * 64 + lane];
+            ql[rt][b] = s_q[((rt * 8 + b) * 2 + 1) * 64 + lane];
         }
-    }
 
     // rows of this lane (S^T layout, column i16): query qt, head hh, last visible key qpos (-1: padding row)
     int qpos[RT];
@@ -489,29 +515,73 @@ __device__ __forceinline__ h8 q4_codes(uint32_t w, const Q4Masks& k) {
     return make_h8(e04, e15, e26, e37);
 }
 
-// RT row tiles per wave.  RT = 1 keeps Q in registers; RT = 2 (verify) keeps the Q fragments of both tiles in LDS
-// (shared by the 4 waves), so each chunk's K codes and V operands are unpacked once for both tiles while the wave
-// still fits two per SIMD.  A row's arithmetic is the same whatever RT is.
-template <int NST, int RT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// Merge of the partial states of the WGW waves of a workgroup, split across the waves by head dims: every wave puts
+// its state in LDS, then wave w folds the WGW states of the output tiles TPW w .. TPW w + TPW - 1 (TPW = 16 / WGW)
+// in the fixed tree fold(fold(c0, c1), fold(c2, c3)) (and fold(that, the same over c4..c7) for 8 waves).  Every
+// wave folds (m, l) along the same tree, so all of them hold the merged m and l.
+template <int WGW>
+struct MergeLdsN {
+    f4 o[WGW][16][64];
+    float ml[WGW][2][64];
+};
+
+template <int WGW>
+__device__ __forceinline__ void merge_split(MergeLdsN<WGW>& s, int wave, int lane, float& m, float& l, const f4* o,
+                                            f4* om) {
+    constexpr int TPW = 16 / WGW;
+    __syncthreads();  // every wave is done with the ring (or with the previous tile's merge)
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++) s.o[wave][dt][lane] = o[dt];
+    s.ml[wave][0][lane] = m;
+    s.ml[wave][1][lane] = l;
+    __syncthreads();
+    float mm[WGW], ll[WGW];
+    f4 oo[WGW][TPW];
+#pragma unroll
+    for (int w = 0; w < WGW; w++) {
+        mm[w] = s.ml[w][0][lane];
+        ll[w] = s.ml[w][1][lane];
+#pragma unroll
+        for (int t = 0; t < TPW; t++) oo[w][t] = s.o[w][TPW * wave + t][lane];
+    }
+    // pairwise tree: level k folds state i with state i + 2^k into state i
+#pragma unroll
+    for (int step = 1; step < WGW; step *= 2)
+#pragma unroll
+        for (int w = 0; w < WGW; w += 2 * step) fold<TPW>(mm[w], ll[w], oo[w], mm[w + step], ll[w + step], oo[w + step]);
+    m = mm[0];
+    l = ll[0];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) om[t] = oo[0][t];
+}
+
+// RT row tiles per wave, WGW waves per workgroup (WGW classes, one record).  RT = 1 keeps Q in registers; RT = 2
+// (verify) keeps the Q fragments of both tiles in LDS (shared by the waves), so each chunk's K codes and V operands
+// are unpacked once for both tiles while the wave still fits two per SIMD.  A row's arithmetic is the same whatever
+// RT is.
+template <int NST, int RT, int WGW>
+__global__ void __launch_bounds__(WGW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work) {
     constexpr bool QLDS = RT > 1;
     __shared__ __attribute__((aligned(16))) union {
-        uint8_t ring[WG_CLASSES][NST][Q4Chunk::BYTES];
-        MergeLds merge;
+        struct {
+            h8 q[RT * 8 * 2 * 64];  // [rt][block][hi, lo][lane]
+            uint8_t ring[WGW][NST][Q4Chunk::BYTES];
+        } a;
+        MergeLdsN<WGW> merge;
     } s_u;
-    __shared__ __attribute__((aligned(16))) h8 s_q[QLDS ? RT * 8 * 2 * 64 : 1];  // [rt][block][hi, lo][lane]
+    h8* s_q = s_u.a.q;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
     const int g = blockIdx.y, rec = blockIdx.x;
     const int kmax = pos0 + nq - 1;
     const int nchunk = kmax / CHUNK + 1;
-    const int cls = rec * WG_CLASSES + wave;
+    const int cls = rec * WGW + wave;
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;
     const size_t rowbase = (size_t)g * kv.capacity;
 
-    uint8_t(*ring)[Q4Chunk::BYTES] = s_u.ring[wave];
+    uint8_t(*ring)[Q4Chunk::BYTES] = s_u.a.ring[wave];
     const Q4Offsets off = q4_offsets(lane);
     auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * j); };
     auto issue = [&](int j) {
@@ -520,12 +590,12 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
         if (kb + CHUNK - 1 <= kmax) q4_issue_full(dst, kv, rowbase + kb, off, lane);
         else q4_issue_tail(dst, kv, rowbase, kb, kmax, lane);
     };
-    // the first chunk's loads go out before the Q set-up, so their latency overlaps it (the Q loads complete after
-    // them); the rest of the ring follows the set-up, so the first iteration waits for chunk 0 only
+    // the first chunk's loads go out before the Q set-up, so their latency overlaps it; the rest of the ring follows
+    // the set-up, so the first iteration waits for chunk 0 only
     if (nmine > 0) issue(0);
 
-    // Q / 16 as fp16 hi + lo, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + k_perm(j)
-    h8 qh[QLDS ? 1 : RT][8], ql[QLDS ? 1 : RT][8];
+    // Q / 16 as fp16 hi + lo fragments, loaded once per workgroup
+    q_frags_to_lds<QWA_KV_Q4_0, RT>(q, nq, g, rt0, s_q);
     int qt[RT], hh[RT], qpos[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
@@ -533,30 +603,16 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
         qt[rt] = r / GRP;
         hh[rt] = r % GRP;
         qpos[rt] = qt[rt] < nq ? pos0 + qt[rt] : -1;  // last visible key of this lane's row (-1: padding row)
-        if (QLDS && wave != rt) continue;  // with Q in LDS, wave rt fills tile rt's fragments
-        const float* src = q + ((size_t)(qt[rt] < nq ? qt[rt] : 0) * NH + g * GRP + hh[rt]) * HD + 8 * lg;
+    }
+    __syncthreads();
+    h8 qh[QLDS ? 1 : RT][8], ql[QLDS ? 1 : RT][8];
+    if constexpr (!QLDS) {
 #pragma unroll
         for (int b = 0; b < 8; b++) {
-            const float4 a = *reinterpret_cast<const float4*>(src + 32 * b);
-            const float4 c = *reinterpret_cast<const float4*>(src + 32 * b + 4);
-            const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-            h8 hi, lo;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float v = qt[rt] < nq ? x[k_perm<QWA_KV_Q4_0>(j)] * 0.0625f : 0.0f;
-                hi[j] = (_Float16)v;
-                lo[j] = (_Float16)(v - (float)hi[j]);
-            }
-            if constexpr (QLDS) {
-                s_q[((rt * 8 + b) * 2 + 0) * 64 + lane] = hi;
-                s_q[((rt * 8 + b) * 2 + 1) * 64 + lane] = lo;
-            } else {
-                qh[QLDS ? 0 : rt][b] = hi;
-                ql[QLDS ? 0 : rt][b] = lo;
-            }
+            qh[0][b] = s_q[(b * 2 + 0) * 64 + lane];
+            ql[0][b] = s_q[(b * 2 + 1) * 64 + lane];
         }
     }
-    if constexpr (QLDS) __syncthreads();
     f4 o[RT][16];
     float m[RT], l[RT], msl[RT], mthr[RT];  // msl = m * log2(e) (0 while m = -inf), mthr = m + RESCALE_T
 #pragma unroll
@@ -722,26 +778,26 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
         }
     }
 
-    // ---- merge the 4 classes of each row tile; wave 0 writes the records.  Lane (row i16, lg), tile 2 b + par,
-    // element i holds dim 32 b + 8 lg + 2 i + par.
+    // ---- merge the WGW classes of each row tile, split across the waves by head dims; every wave writes its dims of
+    // the records.  Lane (row i16, lg), tile 2 b + par, element i holds dim 32 b + 8 lg + 2 i + par.
+    constexpr int TPW = 16 / WGW;
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
-        if (merge4(s_u.merge, wave, lane, m[rt], l[rt], o[rt])) {
-            const float lt = half4_sum(l[rt]);
-            if (qpos[rt] >= 0) {
-                float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt[rt]) * GRP + hh[rt]) * REC;
-                if (lg == 0) {
-                    recp[0] = m[rt];
-                    recp[1] = lt;
-                }
+        f4 om[TPW];
+        merge_split<WGW>(s_u.merge, wave, lane, m[rt], l[rt], o[rt], om);
+        const float lt = half4_sum(l[rt]);
+        if (qpos[rt] >= 0) {
+            float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt[rt]) * GRP + hh[rt]) * REC;
+            if (wave == 0 && lg == 0) {
+                recp[0] = m[rt];
+                recp[1] = lt;
+            }
 #pragma unroll
-                for (int b = 0; b < 8; b++) {
-                    float* dst = recp + 4 + 32 * b + 8 * lg;
-                    *reinterpret_cast<float4*>(dst) =
-                        make_float4(o[rt][2 * b][0], o[rt][2 * b + 1][0], o[rt][2 * b][1], o[rt][2 * b + 1][1]);
-                    *reinterpret_cast<float4*>(dst + 4) =
-                        make_float4(o[rt][2 * b][2], o[rt][2 * b + 1][2], o[rt][2 * b][3], o[rt][2 * b + 1][3]);
-                }
+            for (int t = 0; t < TPW; t += 2) {
+                const int b = (TPW * wave + t) >> 1;
+                float* dst = recp + 4 + 32 * b + 8 * lg;
+                *reinterpret_cast<float4*>(dst) = make_float4(om[t][0], om[t + 1][0], om[t][1], om[t + 1][1]);
+                *reinterpret_cast<float4*>(dst + 4) = make_float4(om[t][2], om[t + 1][2], om[t][3], om[t + 1][3]);
             }
         }
     }
@@ -838,6 +894,11 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
     }
 }
 
+// Q4_0 decode workgroups: 8 waves, i.e. one workgroup per CU whose two waves on each SIMD belong to it (with two
+// 4-wave workgroups per CU the SIMD arbiter favours the older workgroup's waves for the whole kernel, and the younger
+// workgroup finishes alone at one wave per SIMD)
+constexpr int Q4_WGW = 8;
+
 template <int KVT>
 static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int nq, int nrec, float* work,
                            hipStream_t st) {
@@ -847,10 +908,10 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
         if constexpr (KVT == QWA_KV_Q4_0) {
             // two row tiles share one pass over the cache; a third tile gets a pass of its own
             if (t + 1 < rt) {
-                hipLaunchKernelGGL((k_dec4<2, 2>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
+                hipLaunchKernelGGL((k_dec4<2, 2, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work);
                 t++;
             } else {
-                hipLaunchKernelGGL((k_dec4<3, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
+                hipLaunchKernelGGL((k_dec4<2, 1, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work);
             }
         } else {
             hipLaunchKernelGGL((k_dec<KVT, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
@@ -862,7 +923,8 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
                          void* work, float* out, const qwa_act_q8* oq, float* out_host, hipStream_t st) {
     // one record per workgroup; workgroups past the last chunk would hold no class with a chunk
     const int nchunk = (pos0 + nq - 1) / CHUNK + 1;
-    const int nsplit = min(NREC, (nchunk + WG_CLASSES - 1) / WG_CLASSES);
+    const int wgw = kvt == QWA_KV_Q4_0 ? Q4_WGW : WG_CLASSES;
+    const int nsplit = min(DEC_CLASSES / wgw, (nchunk + wgw - 1) / wgw);
     float* w = static_cast<float*>(work);
     profile_mark_begin(st);
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, w, st);
