@@ -26,9 +26,9 @@ sys.path.insert(0, HERE)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 METRIC = "decode attn µs/layer + HBM GB/s @150K Q4_0 KV; prefill attn TFLOP/s (1024-tok chunk)"
-# HBM bytes per k_dec4 launch at the headline workload, measured with rocprofv3 PMC counters (read 173.2 MB + write
-# 3.19 MB; the kernel's algorithmic bytes are 172.8 MB)
-KDEC_TRAFFIC = 176.4e6
+# HBM bytes per k_dec4 launch at the headline workload, measured with rocprofv3 PMC counters (read 173.1 MB + write
+# 1.6 MB; the kernel's algorithmic bytes are 172.8 MB)
+KDEC_TRAFFIC = 174.7e6
 BYTES_PER_POS = {0: 4096, 1: 2176, 2: 1152}  # K + V values and scales over the 4 KV heads
 
 
@@ -118,6 +118,7 @@ def main():
         step()
     kern_ms, kern_n = ops.profile_end()
     kern_us = kern_ms * 1000.0 / max(kern_n, 1)
+    kern_dev_us = ops.profile_device_ms() * 1000.0 / max(kern_n, 1)
     us_layer = ms_per_step * 1000.0 / L
     if args.copy_probe:
         src = torch.empty(1 << 27, dtype=torch.float32, device="cuda").fill_(1.0)
@@ -153,6 +154,7 @@ def main():
                                        "512 MiB copy, per k_dec4 dispatch",
                      "kernel": "k_dec4 (split-K Q4_0 decode), average over the timed launches",
                      "kernel_us": round(kern_us, 3), "launches": kern_n,
+                     "kernel_us_device_clock": round(kern_dev_us, 3),
                      "algorithmic_bytes_per_launch": bytes_layer},
     }
 
@@ -198,6 +200,7 @@ def main():
             ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16)
         pk_ms, pk_n = ops.profile_end()
         extra["prefill_kernel_ms"] = round(pk_ms / max(pk_n, 1), 4)
+        extra["prefill_kernel_ms_device_clock"] = round(ops.profile_device_ms() / max(pk_n, 1), 4)
         flop = 4.0 * 24 * 256 * sum(p0 + t + 1 for t in range(B))
         tflops = flop / (ms * 1e-3) / 1e12
         extra["prefill_1024_at_32768_ms"] = round(ms, 4)

@@ -133,12 +133,17 @@ int qwa_kv_pack(const qwa_kv_layer* kv, int kvt, int n_pos, void* dst, void* str
 int qwa_kv_unpack(const void* src, const qwa_kv_layer* kv, int kvt, int n_pos, void* stream);
 
 /* Opt-in kernel timing (no reference counterpart; the reference times phases with env-gated GPU timers,
- * src/runtime/engine.cpp:2477-2480): between qwa_profile_begin() and qwa_profile_end(), every attention call records
- * HIP events around its main kernel (decode: the split-K kernel; prefill: the MFMA kernel).  qwa_profile_end()
- * synchronizes those events and returns the summed kernel time in ms and the number of timed launches.  At most
- * 65536 launches per window; events are created on first use and kept by the library. */
+ * src/runtime/engine.cpp:2477-2480): between qwa_profile_begin() and qwa_profile_end(), every launch of an
+ * attention call's main kernel (decode: the split-K kernel; prefill: the MFMA kernel) is bracketed by two HIP events
+ * on its stream, and each of its workgroups records the device's realtime clock when it starts and ends.
+ * qwa_profile_end() synchronizes the device and returns the summed event-to-event kernel time in ms and the number
+ * of timed launches; qwa_profile_device_ms() then returns the same window's summed device-clock time (per launch:
+ * last workgroup end - first workgroup start), which excludes the dispatch and completion latency the events include.
+ * At most 4096 launches per window; the first qwa_profile_begin() allocates the stamp buffer (64 MiB), and events are
+ * created on first use; the library keeps both. */
 int qwa_profile_begin(void);
 int qwa_profile_end(double* total_ms, int* launches);
+int qwa_profile_device_ms(double* total_ms);
 
 /* Human-readable text of a status code, and of the last error recorded by this library in the calling thread. */
 const char* qwa_status_string(int status);

@@ -239,7 +239,9 @@ template <int KVT, int RT> struct DecCfg {
 // in every pass and every grouping).
 template <int KVT, int RT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work) {
+k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
+      unsigned long long* prof) {
+    prof_start(prof);
     using C = ChunkLds<KVT>;
     constexpr int NST = DecCfg<KVT, RT>::NST;
     // the chunk ring of every wave while streaming; two partial states while merging
@@ -422,6 +424,7 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
             }
         }
     }
+    prof_end(prof);
 }
 
 // ---------------------------------------------------------------------------------------------- Q4_0 decode
@@ -561,7 +564,9 @@ __device__ __forceinline__ void merge_split(MergeLdsN<WGW>& s, int wave, int lan
 // RT is.
 template <int NST, int RT, int WGW>
 __global__ void __launch_bounds__(WGW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work) {
+k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
+       unsigned long long* prof) {
+    prof_start(prof);
     constexpr bool QLDS = RT > 1;
     __shared__ __attribute__((aligned(16))) union {
         struct {
@@ -801,6 +806,7 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
             }
         }
     }
+    prof_end(prof);
 }
 
 // Combine: one workgroup per (query t, head h, quarter of the head dims).  256 threads = 64 dims x 4 slices.
@@ -905,17 +911,21 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
     const int rt = (GRP * nq + 15) / 16;
     const dim3 grid(nrec, NKV);
     for (int t = 0; t < rt; t++) {
+        unsigned long long* prof = profile_slot(nrec * NKV, st);
         if constexpr (KVT == QWA_KV_Q4_0) {
             // two row tiles share one pass over the cache; a third tile gets a pass of its own
             if (t + 1 < rt) {
-                hipLaunchKernelGGL((k_dec4<2, 2, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work);
+                hipLaunchKernelGGL((k_dec4<2, 2, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work,
+                                   prof);
                 t++;
             } else {
-                hipLaunchKernelGGL((k_dec4<2, 1, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work);
+                hipLaunchKernelGGL((k_dec4<2, 1, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work,
+                                   prof);
             }
         } else {
-            hipLaunchKernelGGL((k_dec<KVT, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work);
+            hipLaunchKernelGGL((k_dec<KVT, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work, prof);
         }
+        profile_launched(prof, st);
     }
 }
 
@@ -926,11 +936,9 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     const int wgw = kvt == QWA_KV_Q4_0 ? Q4_WGW : WG_CLASSES;
     const int nsplit = min(DEC_CLASSES / wgw, (nchunk + wgw - 1) / wgw);
     float* w = static_cast<float*>(work);
-    profile_mark_begin(st);
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, w, st);
     else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, w, st);
     else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, w, st);
-    profile_mark_end(st);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const qwa_act_q8 a = oq ? *oq : qwa_act_q8{nullptr, nullptr, nullptr};

@@ -30,7 +30,10 @@ namespace qwa {
 constexpr int PF_WAVES = QWA_PF_WAVES;           // MFMA waves per workgroup
 constexpr int PF_THREADS = PF_WAVES * 64;
 constexpr int PF_WPE = PF_WAVES / 4;             // waves per SIMD
-constexpr int PF_RT = 16 / PF_WAVES > 0 ? 16 / PF_WAVES : 1;  // 16-row MFMA tiles per wave
+#ifndef QWA_PF_RT
+#define QWA_PF_RT (16 / PF_WAVES > 0 ? 16 / PF_WAVES : 1)
+#endif
+constexpr int PF_RT = QWA_PF_RT;                 // 16-row MFMA tiles per wave
 constexpr int PF_ROWS = PF_WAVES * PF_RT * 16;   // rows per workgroup
 constexpr int PF_TILE = 32;                      // keys per tile
 constexpr int PF_KT = PF_TILE / 16;              // 16-key MFMA tiles per tile
@@ -250,7 +253,8 @@ __device__ __forceinline__ float rows_sum(float x) {
 // p0 .. p0 + B - 1.
 template <int KVT>
 __global__ void __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(PF_WPE, PF_WPE)))
-k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0) {
+k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, unsigned long long* prof) {
+    prof_start(prof);
     using L = PfRaw<KVT>;
     __shared__ __attribute__((aligned(16))) uint8_t s_raw[L::NBUF][L::BYTES];
     __shared__ __attribute__((aligned(16))) _Float16 s_k[2][PF_TILE * KS_LD];
@@ -448,6 +452,7 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0) {
         for (int dt = 0; dt < 16; dt++)
             dst[4 * dt + lg] = make_float4(o[rt][dt][0], o[rt][dt][1], o[rt][dt][2], o[rt][dt][3]);
     }
+    prof_end(prof);
 }
 
 // Merges the PF_NS partial states of each output row in split order, normalises, applies the sigmoid gate and
@@ -486,22 +491,22 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ ga
 
 hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
                           uint16_t* out16, hipStream_t st) {
-    profile_mark_begin(st);
     for (int t0 = 0; t0 < B; t0 += PF_MAXB) {
         const int nb = min(PF_MAXB, B - t0);
         const float* qp = q + (size_t)t0 * NH * HD;
         const dim3 grid((GRP * nb + PF_ROWS - 1) / PF_ROWS, NKV, PF_NS);
+        unsigned long long* prof = profile_slot(grid.x * grid.y * grid.z, st);
         if (kvt == QWA_KV_F16)
-            hipLaunchKernelGGL(k_prefill<QWA_KV_F16>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0);
+            hipLaunchKernelGGL(k_prefill<QWA_KV_F16>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0, prof);
         else if (kvt == QWA_KV_Q8_0)
-            hipLaunchKernelGGL(k_prefill<QWA_KV_Q8_0>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0);
+            hipLaunchKernelGGL(k_prefill<QWA_KV_Q8_0>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0, prof);
         else
-            hipLaunchKernelGGL(k_prefill<QWA_KV_Q4_0>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0);
+            hipLaunchKernelGGL(k_prefill<QWA_KV_Q4_0>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0, prof);
+        profile_launched(prof, st);
         const int nrows = nb * NH;
         hipLaunchKernelGGL(k_pf_combine, dim3((nrows + 3) / 4), dim3(256), 0, st, gate + (size_t)t0 * NH * HD, nrows,
                            out16 + (size_t)t0 * NH * HD);
     }
-    profile_mark_end(st);
     return hipGetLastError();
 }
 

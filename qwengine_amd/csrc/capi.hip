@@ -1,4 +1,5 @@
-// C ABI (include/qwattn.h): argument validation, then the kernel launchers.  Nothing here allocates memory.
+// C ABI (include/qwattn.h): argument validation, then the kernel launchers.  Nothing here allocates memory, except
+// the opt-in timing window (qwa_profile_begin), which keeps one stamp buffer for the life of the process.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -47,35 +48,37 @@ int check_src(const qwa_row_src* s, int n, const char* what, const char* fn) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-// kernel timing window
-constexpr int PROF_MAX = 65536;
+// kernel timing window: each timed launch gets a slot of per-workgroup (start, end) stamps in a device buffer
+constexpr int PROF_MAX = 4096;     // launches per window
 struct Profile {
     bool on = false;
     int n = 0;
-    std::vector<hipEvent_t> ev;  // 2 per launch, created lazily
+    unsigned long long* stamps = nullptr;  // [PROF_MAX][PROF_MAX_WG][2], allocated on the first window
+    std::vector<int> nwg;                  // workgroups of each timed launch
+    std::vector<hipEvent_t> ev;            // 2 per launch (around it on its stream), created on first use
+    double device_ms = 0.0;                // device-clock total of the last closed window
 } g_prof;
 
 }  // namespace
 
 namespace qwa {
 
-static void prof_record(hipStream_t st, int which) {
-    if (!g_prof.on || g_prof.n >= PROF_MAX) return;
-    const size_t idx = 2 * (size_t)g_prof.n + which;
-    while (g_prof.ev.size() <= idx) {
+unsigned long long* profile_slot(int nwg, hipStream_t st) {
+    if (!g_prof.on || g_prof.stamps == nullptr || g_prof.n >= PROF_MAX || nwg > PROF_MAX_WG) return nullptr;
+    const size_t idx = 2 * (size_t)g_prof.n;
+    while (g_prof.ev.size() <= idx + 1) {
         hipEvent_t e;
-        if (hipEventCreate(&e) != hipSuccess) {
-            g_prof.on = false;
-            return;
-        }
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
         g_prof.ev.push_back(e);
     }
-    hipEventRecord(g_prof.ev[idx], st);
-    if (which == 1) g_prof.n++;
+    if (hipEventRecord(g_prof.ev[idx], st) != hipSuccess) return nullptr;
+    g_prof.nwg.push_back(nwg);
+    return g_prof.stamps + (size_t)g_prof.n++ * PROF_MAX_WG * 2;
 }
 
-void profile_mark_begin(hipStream_t st) { prof_record(st, 0); }
-void profile_mark_end(hipStream_t st) { prof_record(st, 1); }
+void profile_launched(unsigned long long* slot, hipStream_t st) {
+    if (slot != nullptr) (void)hipEventRecord(g_prof.ev[2 * (size_t)(g_prof.n - 1) + 1], st);
+}
 
 }  // namespace qwa
 
@@ -264,25 +267,63 @@ int qwa_kv_unpack(const void* src, const qwa_kv_layer* kv, int kvt, int n_pos, v
 }
 
 int qwa_profile_begin(void) {
+    const size_t bytes = (size_t)PROF_MAX * qwa::PROF_MAX_WG * 2 * sizeof(unsigned long long);
+    if (g_prof.stamps == nullptr) {
+        const hipError_t e = hipMalloc(&g_prof.stamps, bytes);
+        if (e != hipSuccess) {
+            g_prof.stamps = nullptr;
+            return from_hip(e, "profile_begin");
+        }
+    }
+    const hipError_t e = hipMemset(g_prof.stamps, 0, bytes);
+    if (e != hipSuccess) return from_hip(e, "profile_begin");
     g_prof.on = true;
     g_prof.n = 0;
+    g_prof.nwg.clear();
     return QWA_OK;
 }
 
 int qwa_profile_end(double* total_ms, int* launches) {
     g_prof.on = false;
-    double tot = 0.0;
-    for (int i = 0; i < g_prof.n; i++) {
-        hipError_t e = hipEventSynchronize(g_prof.ev[2 * i + 1]);
+    double tot = 0.0, dev_tot = 0.0;
+    const int n = g_prof.n;
+    g_prof.device_ms = 0.0;
+    if (n > 0) {
+        hipError_t e = hipDeviceSynchronize();
         if (e != hipSuccess) return from_hip(e, "profile_end");
-        float ms = 0.0f;
-        e = hipEventElapsedTime(&ms, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]);
+        int dev = 0, khz = 0;
+        e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
         if (e != hipSuccess) return from_hip(e, "profile_end");
-        tot += ms;
+        if (khz <= 0) return fail(QWA_ERR_HIP, "profile_end: no wall-clock rate");
+        std::vector<unsigned long long> h((size_t)n * qwa::PROF_MAX_WG * 2);
+        e = hipMemcpy(h.data(), g_prof.stamps, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return from_hip(e, "profile_end");
+        for (int i = 0; i < n; i++) {
+            const unsigned long long* st = h.data() + (size_t)i * qwa::PROF_MAX_WG * 2;
+            unsigned long long t0 = ~0ull, t1 = 0;
+            for (int w = 0; w < g_prof.nwg[i]; w++) {
+                if (st[2 * w] == 0 || st[2 * w + 1] == 0) return fail(QWA_ERR_HIP, "profile_end: missing stamp");
+                t0 = st[2 * w] < t0 ? st[2 * w] : t0;
+                t1 = st[2 * w + 1] > t1 ? st[2 * w + 1] : t1;
+            }
+            dev_tot += (double)(t1 - t0) / (double)khz;  // ticks / kHz = ms
+            float ms = 0.0f;
+            e = hipEventElapsedTime(&ms, g_prof.ev[2 * (size_t)i], g_prof.ev[2 * (size_t)i + 1]);
+            if (e != hipSuccess) return from_hip(e, "profile_end");
+            tot += ms;
+        }
     }
+    g_prof.device_ms = dev_tot;
     if (total_ms) *total_ms = tot;
-    if (launches) *launches = g_prof.n;
+    if (launches) *launches = n;
     g_prof.n = 0;
+    g_prof.nwg.clear();
+    return QWA_OK;
+}
+
+int qwa_profile_device_ms(double* total_ms) {
+    if (total_ms) *total_ms = g_prof.device_ms;
     return QWA_OK;
 }
 

@@ -7,9 +7,26 @@
 
 namespace qwa {
 
-// opt-in kernel timing (qwa_profile_begin / qwa_profile_end): marks around a main kernel launch
-void profile_mark_begin(hipStream_t st);
-void profile_mark_end(hipStream_t st);
+// opt-in kernel timing (qwa_profile_begin / qwa_profile_end): before a main kernel launch of nwg workgroups the
+// launcher asks for a slot of 2 * nwg stamps (nullptr when timing is off; a HIP event is recorded on the stream), and
+// after the launch reports it (a second event); wave 0 of workgroup w writes the realtime clock at its start to
+// slot[2 w] and, after the workgroup's last store, at its end to slot[2 w + 1]
+constexpr int PROF_MAX_WG = 1024;
+unsigned long long* profile_slot(int nwg, hipStream_t st);
+void profile_launched(unsigned long long* slot, hipStream_t st);
+
+__device__ __forceinline__ int prof_wg() { return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); }
+// (wave 0 stores with all its lanes: a wave-uniform branch keeps the kernels' scalar operands uniform)
+__device__ __forceinline__ bool prof_wave0() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) == 0; }
+__device__ __forceinline__ void prof_start(unsigned long long* prof) {
+    if (prof != nullptr && prof_wave0()) prof[2 * prof_wg()] = __builtin_amdgcn_s_memrealtime();
+}
+__device__ __forceinline__ void prof_end(unsigned long long* prof) {
+    if (prof != nullptr) {
+        __syncthreads();
+        if (prof_wave0()) prof[2 * prof_wg() + 1] = __builtin_amdgcn_s_memrealtime();
+    }
+}
 
 hipError_t launch_prep(const qwa_row_src& qg, const qwa_row_src& k, const qwa_row_src& v, const float* qn,
                        const float* kn, int pos0, int rpos0, int n, float theta, float eps, int kvt,

@@ -80,6 +80,7 @@ EXPORTS = {
                                      ctypes.c_void_p]),
     "qwa_profile_begin": (ctypes.c_int, []),
     "qwa_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
+    "qwa_profile_device_ms": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double)]),
     "qwa_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "qwa_last_error": (ctypes.c_char_p, []),
 }
@@ -294,11 +295,19 @@ def profile_begin() -> None:
 
 
 def profile_end() -> tuple[float, int]:
-    """Stop timing; returns (summed main-kernel time in ms, number of timed launches)."""
+    """Stop timing; returns (summed main-kernel time in ms from the HIP events around each launch, number of timed
+    launches)."""
     ms = ctypes.c_double(0.0)
     n = ctypes.c_int(0)
     _check(lib().qwa_profile_end(ctypes.byref(ms), ctypes.byref(n)))
     return ms.value, n.value
+
+
+def profile_device_ms() -> float:
+    """Summed device-clock time of the last closed window (first workgroup start to last workgroup end per launch)."""
+    ms = ctypes.c_double(0.0)
+    _check(lib().qwa_profile_device_ms(ctypes.byref(ms)))
+    return ms.value
 
 
 def kv_packed_bytes(kvt, n_pos: int) -> int:
