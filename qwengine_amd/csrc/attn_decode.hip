@@ -748,22 +748,43 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
             }
         };
 
-        for (int j = 0; j < nmine; j++) {
-            if (j + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
+        if constexpr (RT == 1) {
+            // software-pipelined: iteration j multiplies chunk j's V while it scores chunk j + 1, so the two chunks'
+            // MFMA and VALU chains interleave within the wave.  Per row the operations and their order are those of
+            // one chunk after the other: the P.V of chunk j, then the softmax of chunk j + 1, whose rescale covers it.
+            if (NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
             else wait_vmcnt<0>();
-            if constexpr (RT == 1) {
+            h4 P[1];
+            VRegs vr;
+            {
                 KRegs kr;
-                read_k(j, kr);
-                VRegs vr;
-                read_v(j, vr);
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot j is read out: refill it
-                if (j + NST < nmine) issue(j + NST);
-                f4 S[RT];
+                read_k(0, kr);
+                f4 S[1];
                 scores(kr, S);
-                h4 P[RT];
-                P[0] = softmax(j, S[0], 0);
+                P[0] = softmax(0, S[0], 0);
+                read_v(0, vr);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot 0 is read out: refill it
+                if (NST < nmine) issue(NST);
+            }
+            for (int j = 0; j + 1 < nmine; j++) {
+                if (j + 1 + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();
+                else wait_vmcnt<0>();
+                KRegs kr;
+                read_k(j + 1, kr);
+                f4 S[1];
                 pv(vr, P);
-            } else {
+                scores(kr, S);
+                const h4 Pn = softmax(j + 1, S[0], 0);
+                read_v(j + 1, vr);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot j + 1 is read out: refill it
+                if (j + 1 + NST < nmine) issue(j + 1 + NST);
+                P[0] = Pn;
+            }
+            pv(vr, P);
+        } else {
+            for (int j = 0; j < nmine; j++) {
+                if (j + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
+                else wait_vmcnt<0>();
                 // two row tiles: V is read after the softmax, so K and V registers are never live together
                 f4 S[RT];
                 {
