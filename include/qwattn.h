@@ -139,8 +139,8 @@ int qwa_kv_unpack(const void* src, const qwa_kv_layer* kv, int kvt, int n_pos, v
  * qwa_profile_end() synchronizes the device and returns the summed event-to-event kernel time in ms and the number
  * of timed launches; qwa_profile_device_ms() then returns the same window's summed device-clock time (per launch:
  * last workgroup end - first workgroup start), which excludes the dispatch and completion latency the events include.
- * At most 4096 launches per window; the first qwa_profile_begin() allocates the stamp buffer (64 MiB), and events are
- * created on first use; the library keeps both. */
+ * At most 1024 launches of at most 4096 workgroups per window; the first qwa_profile_begin() allocates the stamp
+ * buffer (64 MiB), and events are created on first use; the library keeps both. */
 int qwa_profile_begin(void);
 int qwa_profile_end(double* total_ms, int* launches);
 int qwa_profile_device_ms(double* total_ms);

@@ -49,7 +49,7 @@ int check_src(const qwa_row_src* s, int n, const char* what, const char* fn) {
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 // kernel timing window: each timed launch gets a slot of per-workgroup (start, end) stamps in a device buffer
-constexpr int PROF_MAX = 4096;     // launches per window
+constexpr int PROF_MAX = 1024;     // launches per window
 struct Profile {
     bool on = false;
     int n = 0;

@@ -11,7 +11,7 @@ namespace qwa {
 // launcher asks for a slot of 2 * nwg stamps (nullptr when timing is off; a HIP event is recorded on the stream), and
 // after the launch reports it (a second event); wave 0 of workgroup w writes the realtime clock at its start to
 // slot[2 w] and, after the workgroup's last store, at its end to slot[2 w + 1]
-constexpr int PROF_MAX_WG = 1024;
+constexpr int PROF_MAX_WG = 4096;
 unsigned long long* profile_slot(int nwg, hipStream_t st);
 void profile_launched(unsigned long long* slot, hipStream_t st);
 
