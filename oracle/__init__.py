@@ -71,6 +71,8 @@ def lib():
     L.qwo_rope_table_pos.argtypes = [_i32p, ctypes.c_int, ctypes.c_float, _f32p]
     L.qwo_act_q8.argtypes = [_f32p, _i64, _i8p, _f32p, _f32p]
     L.qwo_max_threads.restype = ctypes.c_int
+    L.qwo_deltanet.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p, _f32p,
+                               ctypes.c_float, _f32p, _f32p, _f32p]
     _lib = L
     return L
 
@@ -219,6 +221,28 @@ def act_q8(v):
     s = np.empty(v.size // 32, np.float32)
     lib().qwo_act_q8(v, v.size, q, d, s)
     return q, d, s
+
+
+# ---- Gated DeltaNet core (src/reference/ref_model.cpp:169-256) ----
+DN_CH, DN_QK, DN_V, DN_VH, DN_KH, DN_HD = 10240, 2048, 6144, 48, 16, 128
+
+
+def deltanet(qkv, z, b, a, conv_w, dt_bias, ssm_a, ssm_norm, eps, conv_state, S):
+    """T tokens of one Gated DeltaNet layer from its projection outputs: qkv [T][10240], z [T][6144], b / a [T][48]
+    (raw beta / alpha), conv_w [10240][4], dt_bias / ssm_a [48], ssm_norm [128], conv_state [3][10240] (oldest input
+    first), S [48][128 i][128 j] (i = key index).  Returns (o [T][6144], new conv_state, new S); inputs unchanged."""
+    qkv = _f32(qkv).reshape(-1, DN_CH)
+    T = qkv.shape[0]
+    z = _f32(z).reshape(T, DN_V)
+    b = _f32(b).reshape(T, -1)
+    a = _f32(a).reshape(T, -1)
+    assert b.shape == a.shape and b.shape[1] >= DN_VH
+    cs = _f32(conv_state).reshape(3, DN_CH).copy()
+    St = _f32(S).reshape(DN_VH, DN_HD, DN_HD).copy()
+    o = np.empty((T, DN_V), np.float32)
+    lib().qwo_deltanet(qkv, z, b, a, b.shape[1], T, _f32(conv_w).reshape(-1), _f32(dt_bias), _f32(ssm_a),
+                       _f32(ssm_norm), eps, cs.reshape(-1), St.reshape(-1), o.reshape(-1))
+    return o, cs, St
 
 
 def max_threads() -> int:

@@ -407,3 +407,90 @@ void qwo_act_q8(const float* v, int64_t n, int8_t* q, float* d, float* s) {
 }
 
 int qwo_max_threads(void) { return omp_get_max_threads(); }
+
+
+/* ---- Gated DeltaNet core: src/reference/ref_model.cpp:169-256 (helpers rmsnorm / sigmoidf / siluf / softplusf at
+ * :41-50).  Same statement order as the reference's token loop. */
+static float dn_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+static float dn_silu(float x) { return x / (1.0f + expf(-x)); }
+static float dn_softplus(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+
+static void dn_rmsnorm(const float* x, const float* w, float* y, int n, float eps) {
+    double ss = 0;
+    for (int i = 0; i < n; i++) ss += (double)x[i] * x[i];
+    const float scale = 1.0f / sqrtf((float)(ss / n) + eps);
+    for (int i = 0; i < n; i++) y[i] = x[i] * scale * w[i];
+}
+
+void qwo_deltanet(const float* qkv, const float* z, const float* b, const float* a, int ld_ba, int T,
+                  const float* conv_w, const float* dt_bias, const float* ssm_a, const float* ssm_norm, float eps,
+                  float* conv_state, float* S, float* o) {
+    enum { CH = QWO_DN_CH, QK = QWO_DN_QK, VD = QWO_DN_V, VH = QWO_DN_VH, KH = QWO_DN_KH, HD = QWO_DN_HD };
+    float* conv = (float*)malloc(sizeof(float) * CH);
+    float* qn = (float*)malloc(sizeof(float) * QK);
+    float* kn = (float*)malloc(sizeof(float) * QK);
+    float* cs = conv_state;
+    for (int t = 0; t < T; t++) {
+        const float* x = qkv + (size_t)t * CH;
+        /* causal conv (width 4) + SiLU, the window slides by one input (ref_model.cpp:191-200) */
+        for (int c = 0; c < CH; c++) {
+            const float* w = conv_w + (size_t)c * 4;
+            const float acc = w[0] * cs[0 * CH + c] + w[1] * cs[1 * CH + c] + w[2] * cs[2 * CH + c] + w[3] * x[c];
+            conv[c] = dn_silu(acc);
+            cs[0 * CH + c] = cs[1 * CH + c];
+            cs[1 * CH + c] = cs[2 * CH + c];
+            cs[2 * CH + c] = x[c];
+        }
+        /* L2 normalization of q and k per key head, sums in double (ref_model.cpp:202-215) */
+        for (int h = 0; h < KH; h++) {
+            double sq = 0, sk = 0;
+            for (int d = 0; d < HD; d++) {
+                sq += (double)conv[h * HD + d] * conv[h * HD + d];
+                sk += (double)conv[QK + h * HD + d] * conv[QK + h * HD + d];
+            }
+            const float sqf = (float)sqrt(sq), skf = (float)sqrt(sk);
+            const float iq = 1.0f / (sqf > eps ? sqf : eps);
+            const float ik = 1.0f / (skf > eps ? skf : eps);
+            for (int d = 0; d < HD; d++) {
+                qn[h * HD + d] = conv[h * HD + d] * iq;
+                kn[h * HD + d] = conv[QK + h * HD + d] * ik;
+            }
+        }
+        const float* vv = conv + 2 * QK;
+        const float qscale = 1.0f / sqrtf((float)HD);
+#pragma omp parallel for
+        for (int h = 0; h < VH; h++) {
+            const int kh = h % KH;
+            const float beta = dn_sigmoid(b[(size_t)t * ld_ba + h]);
+            const float g = dn_softplus(a[(size_t)t * ld_ba + h] + dt_bias[h]) * ssm_a[h];
+            const float decay = expf(g);
+            float* Sh = S + (size_t)h * HD * HD; /* Sh[i * 128 + j]: i = k index, j = v index */
+            const float* kk = kn + kh * HD;
+            const float* qq = qn + kh * HD;
+            const float* vh = vv + h * HD;
+            float kv[HD], delta[HD], oh[HD];
+            for (int j = 0; j < HD; j++) kv[j] = 0.0f;
+            for (int i = 0; i < HD; i++)
+                for (int j = 0; j < HD; j++) {
+                    Sh[i * HD + j] *= decay;
+                    kv[j] += Sh[i * HD + j] * kk[i];
+                }
+            for (int j = 0; j < HD; j++) delta[j] = (vh[j] - kv[j]) * beta;
+            for (int j = 0; j < HD; j++) oh[j] = 0.0f;
+            for (int i = 0; i < HD; i++)
+                for (int j = 0; j < HD; j++) {
+                    Sh[i * HD + j] += kk[i] * delta[j];
+                    oh[j] += Sh[i * HD + j] * qq[i];
+                }
+            /* gated RMSNorm: rmsnorm(o_h / sqrt(128)) * ssm_norm * silu(z_h) (ref_model.cpp:245-252) */
+            float* od = o + (size_t)t * VD + h * HD;
+            for (int j = 0; j < HD; j++) oh[j] *= qscale;
+            dn_rmsnorm(oh, ssm_norm, od, HD, eps);
+            const float* zh = z + (size_t)t * VD + h * HD;
+            for (int j = 0; j < HD; j++) od[j] *= dn_silu(zh[j]);
+        }
+    }
+    free(conv);
+    free(qn);
+    free(kn);
+}

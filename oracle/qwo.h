@@ -13,6 +13,7 @@
  *   - q/k prep (RMSNorm, RoPE) : src/cuda/ops.cu:309-358, tests/kernels/test_ops.cu:260-272 (double precision)
  *   - RoPE tables              : src/cuda/prefill.cu:385-407
  *   - ActQ8 epilogue           : src/cuda/common.cuh:188-197
+ *   - Gated DeltaNet core      : src/reference/ref_model.cpp:169-256 (after the projections), :41-50 (helpers)
  * Each function below names the reference lines it follows.
  */
 #ifndef QWO_H
@@ -72,6 +73,19 @@ void qwo_rope_table_pos(const int* pos, int B, float theta, float* rope);
 void qwo_act_q8(const float* v, int64_t n, int8_t* q, float* d, float* s);
 
 int qwo_max_threads(void);
+
+/* Gated DeltaNet core of one layer over T tokens (src/reference/ref_model.cpp:169-256, from the projection outputs
+ * on; helpers :41-50).  Per token: causal depthwise conv (width 4) + SiLU over the 10240 q|k|v channels, L2
+ * normalization of the 16 q and k heads (sums in double, clamp eps), per value head h (key head h % 16):
+ * beta = sigmoid(b), decay = exp(softplus(a + dt_bias) * ssm_a), S *= decay, kv = S^T k, delta = (v - kv) * beta,
+ * S += k delta^T, o = S^T q / sqrt(128), then the gated RMSNorm rmsnorm(o) * ssm_norm * silu(z).
+ * qkv [T][10240], z [T][6144], b / a [T][ld_ba] (the first 48 used), conv_w [10240][4], dt_bias / ssm_a [48],
+ * ssm_norm [128].  conv_state [3][10240] (oldest input first) and S [48][128 k index i][128 v index j] are read and
+ * updated in place.  o [T][6144]. */
+enum { QWO_DN_CH = 10240, QWO_DN_QK = 2048, QWO_DN_V = 6144, QWO_DN_VH = 48, QWO_DN_KH = 16, QWO_DN_HD = 128 };
+void qwo_deltanet(const float* qkv, const float* z, const float* b, const float* a, int ld_ba, int T,
+                  const float* conv_w, const float* dt_bias, const float* ssm_a, const float* ssm_norm, float eps,
+                  float* conv_state, float* S, float* o);
 
 #ifdef __cplusplus
 }
