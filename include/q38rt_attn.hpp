@@ -1,6 +1,6 @@
-// q38rt_attn.hpp -- header-only C++ shim that re-creates the reference runtime's attention / KV-cache operator
-// signatures (namespace q38rt::cuda, src/cuda/ops.cuh:99-140 and src/cuda/prefill.cuh:46-62) on top of the C ABI in
-// qwattn.h, so the engine's call sites (src/runtime/engine.cpp:1587-1592, 2457-2479) compile unchanged against the
+// q38rt_attn.hpp -- header-only C++ shim that re-creates the reference runtime's attention / KV-cache and Gated
+// DeltaNet operator signatures (namespace q38rt::cuda, src/cuda/ops.cuh:54-140 and src/cuda/prefill.cuh:37-62) on top
+// of the C ABI in qwattn.h, so the engine's call sites (src/runtime/engine.cpp:1587-1592, 2457-2479) compile unchanged against the
 // MI355X library.  The stream type is hipStream_t; fp16 outputs are uint16_t bits (the reference's __half).
 // Like the reference, a rejected call prints the reason and aborts (src/cuda/ops.cu:1002-1008).
 #pragma once
@@ -53,6 +53,35 @@ struct RowSrc {
     }
 };
 
+// src/cuda/ops.cuh:54-62
+struct DeltaNetParams {
+    const float* conv_w = nullptr;
+    const float* dt_bias = nullptr;
+    const float* ssm_a = nullptr;
+    const float* ssm_norm = nullptr;
+    float* conv_state = nullptr;
+    float* ssm_state = nullptr;
+};
+
+// src/cuda/ops.cuh:74-91 (same defaults: no host part)
+struct DNTokens {
+    const float* sqkv = nullptr;
+    const float* sbeta = nullptr;
+    const float* salpha = nullptr;
+    const float* qkv = nullptr;
+    const float* z = nullptr;
+    const float* beta = nullptr;
+    const float* alpha = nullptr;
+    float* oqkv = nullptr;
+    float* obeta = nullptr;
+    float* oalpha = nullptr;
+    const float* qkv_host = nullptr;
+    int qkv_split = 1 << 30, qkv_ld = 0;
+    const float* z_host = nullptr;
+    int z_split = 1 << 30, z_ld = 0;
+    float* o_host = nullptr;
+};
+
 namespace detail {
 inline void check(int status, const char* fn) {
     if (status != QWA_OK) {
@@ -62,6 +91,13 @@ inline void check(int status, const char* fn) {
 }
 inline qwa_kv_layer c(const KVLayer& kv) { return qwa_kv_layer{kv.k, kv.v, kv.ks, kv.vs, kv.capacity}; }
 inline qwa_row_src c(const RowSrc& s) { return qwa_row_src{s.dev, s.host, s.split, s.host_ld}; }
+inline qwa_dn_params c(const DeltaNetParams& p) {
+    return qwa_dn_params{p.conv_w, p.dt_bias, p.ssm_a, p.ssm_norm, p.conv_state, p.ssm_state};
+}
+inline qwa_dn_tokens c(const DNTokens& t) {
+    return qwa_dn_tokens{t.sqkv, t.sbeta,    t.salpha,    t.qkv,    t.z,       t.beta,   t.alpha, t.oqkv, t.obeta,
+                         t.oalpha, t.qkv_host, t.qkv_split, t.qkv_ld, t.z_host, t.z_split, t.z_ld, t.o_host};
+}
 }  // namespace detail
 
 inline size_t kv_value_bytes(KVType t) { return qwa_kv_value_bytes((int)t); }
@@ -146,6 +182,37 @@ inline void attn_prefill(const float* q, const float* gate, const KVLayer& kv, K
 inline void attn_prefill_simple(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int B, int p0,
                                 __half* out16, hipStream_t st) {
     attn_prefill_simple(q, gate, kv, kvt, B, p0, reinterpret_cast<uint16_t*>(out16), st);
+}
+
+// ---- Gated DeltaNet: src/cuda/ops.cuh:67-68, 96-97; src/cuda/prefill.cuh:41-44
+inline void deltanet_step(const DeltaNetParams& p, const float* qkv, const float* z, const float* beta_raw,
+                          const float* alpha_raw, int parity, float eps, float* o, const ActQ8* oq, hipStream_t st) {
+    const qwa_dn_params cp = detail::c(p);
+    qwa_act_q8 q8{};
+    if (oq) q8 = qwa_act_q8{oq->q, oq->d, oq->s};
+    detail::check(qwa_deltanet_step(&cp, qkv, z, beta_raw, alpha_raw, parity, eps, o, oq ? &q8 : nullptr, st),
+                  "deltanet_step");
+}
+
+inline void deltanet_multi(const DeltaNetParams& p, int cin, const DNTokens& in, int n_commit, int n_new,
+                           int write_after, float eps, float* o, const ActQ8* oq, hipStream_t st) {
+    const qwa_dn_params cp = detail::c(p);
+    const qwa_dn_tokens ct = detail::c(in);
+    qwa_act_q8 q8{};
+    if (oq) q8 = qwa_act_q8{oq->q, oq->d, oq->s};
+    detail::check(qwa_deltanet_multi(&cp, cin, &ct, n_commit, n_new, write_after, eps, o, oq ? &q8 : nullptr, st),
+                  "deltanet_multi");
+}
+
+inline size_t dn_work_bytes(int B) { return qwa_dn_work_bytes(B); }
+
+inline void deltanet_rows(const DeltaNetParams& p, const float* qkv, const float* z, const float* beta_raw,
+                          const float* alpha_raw, int B, int cin, float eps, void* work, float* core_out, __half* o16,
+                          hipStream_t st) {
+    const qwa_dn_params cp = detail::c(p);
+    detail::check(qwa_deltanet_rows(&cp, qkv, z, beta_raw, alpha_raw, B, cin, eps, work, core_out,
+                                    reinterpret_cast<uint16_t*>(o16), st),
+                  "deltanet_rows");
 }
 
 }  // namespace cuda

@@ -1,8 +1,8 @@
 /*
- * qwattn.h -- C ABI of the MI355X (gfx950) gated-attention path.
+ * qwattn.h -- C ABI of the MI355X (gfx950) gated-attention path and of the Gated DeltaNet token mixer.
  *
- * Drop-in replacement for the attention / KV-cache operators of the reference runtime (namespace q38rt::cuda,
- * src/cuda/ops.cuh and src/cuda/prefill.cuh).  Every entry point below names the reference declaration it
+ * Drop-in replacement for the attention / KV-cache and Gated DeltaNet operators of the reference runtime (namespace
+ * q38rt::cuda, src/cuda/ops.cuh and src/cuda/prefill.cuh).  Every entry point below names the reference declaration it
  * replaces.  Conventions:
  *   - all tensors are caller-owned device memory (out_host: host memory mapped for device access);
  *   - `stream` is a hipStream_t (NULL = the default stream); every call is asynchronous and stream-ordered;
@@ -10,7 +10,8 @@
  *   - the return value is a status code (QWA_OK = 0).  Invalid arguments are rejected before anything is launched
  *     (the reference aborts in the same situations, src/cuda/ops.cu:1002-1008); the C++ shim in q38rt_attn.hpp
  *     turns a nonzero status into abort() exactly like the reference.
- * Shapes are fixed by the model: 24 query heads, 4 KV heads (GQA group 6), head_dim 256, 64 rotary dims.
+ * Shapes are fixed by the model: attention 24 query heads, 4 KV heads (GQA group 6), head_dim 256, 64 rotary dims;
+ * Gated DeltaNet 16 key heads, 48 value heads, head dim 128, 10240 conv channels.
  */
 #ifndef QWATTN_H
 #define QWATTN_H
@@ -131,6 +132,72 @@ int qwa_kv_append(const float* xk, const float* xv, int pos0, int n, int kvt, co
 long long qwa_kv_packed_bytes(int kvt, int n_pos);
 int qwa_kv_pack(const qwa_kv_layer* kv, int kvt, int n_pos, void* dst, void* stream);
 int qwa_kv_unpack(const void* src, const qwa_kv_layer* kv, int kvt, int n_pos, void* stream);
+
+/* ---- Gated DeltaNet (the recurrent token mixer of the other layers) ---------------------------------------------- */
+
+/* New tokens per qwa_deltanet_multi call (the reference's DN_MAXN = Engine::MAX_BATCH, src/cuda/ops.cu:148). */
+#define QWA_DN_MAXN 7
+
+/* Parameters of one Gated DeltaNet layer (device pointers).  Replaces q38rt::cuda::DeltaNetParams
+ * (src/cuda/ops.cuh:54-62): conv_w [10240][4], dt_bias [48], ssm_a [48] (= -exp(A_log)), ssm_norm [128],
+ * conv_state [2][3][10240] ping-pong (buffer = parity; rows oldest input first), ssm_state [48][128 col j][128 row i]
+ * fp32 (j = value dim, i = key dim). */
+typedef struct {
+    const float* conv_w;
+    const float* dt_bias;
+    const float* ssm_a;
+    const float* ssm_norm;
+    float* conv_state;
+    float* ssm_state;
+} qwa_dn_params;
+
+/* Token inputs of qwa_deltanet_multi.  Replaces q38rt::cuda::DNTokens (src/cuda/ops.cuh:74-91).  Pending tokens
+ * (output by an earlier pass, applied to the state now): sqkv [n][10240], sbeta / salpha [n][64].  New tokens:
+ * qkv [n][10240], z [n][6144], beta / alpha [n][64] (raw projections; the first 48 of each row are used).
+ * oqkv / obeta / oalpha (optional, NULL when unused) receive the new tokens' inputs for a later commit; they must not
+ * alias the pending inputs.  New tokens' qkv channels >= qkv_split are read from qkv_host [n][qkv_ld] (mapped host
+ * memory), z channels >= z_split from z_host [n][z_ld]; a split of 10240 / 6144 or more means no host part (the
+ * reference's default is 1 << 30).  o_host (optional) receives a copy of the outputs, rows of 6144. */
+typedef struct {
+    const float* sqkv;
+    const float* sbeta;
+    const float* salpha;
+    const float* qkv;
+    const float* z;
+    const float* beta;
+    const float* alpha;
+    float* oqkv;
+    float* obeta;
+    float* oalpha;
+    const float* qkv_host;
+    int qkv_split, qkv_ld;
+    const float* z_host;
+    int z_split, z_ld;
+    float* o_host;
+} qwa_dn_tokens;
+
+/* Replaces deltanet_step (src/cuda/ops.cuh:67-68): one token; the conv window is read from buffer `parity` and
+ * written to buffer parity ^ 1, the state is updated in place.  o [6144] fp32, optional ActQ8 rows. */
+int qwa_deltanet_step(const qwa_dn_params* p, const float* qkv, const float* z, const float* beta_raw,
+                      const float* alpha_raw, int parity, float eps, float* o, const qwa_act_q8* oq, void* stream);
+
+/* Replaces deltanet_multi (src/cuda/ops.cuh:96-97): applies n_commit pending tokens then n_new (<= QWA_DN_MAXN) new
+ * tokens (outputs o [n_new][6144], optional ActQ8 rows); the conv window (to buffer cin ^ 1) and the state (in place)
+ * are written back after `write_after` tokens (0 = leave both unchanged).  Bit-identical to the same tokens applied
+ * one per call.  n_commit + n_new = 0 does nothing. */
+int qwa_deltanet_multi(const qwa_dn_params* p, int cin, const qwa_dn_tokens* in, int n_commit, int n_new,
+                       int write_after, float eps, float* o, const qwa_act_q8* oq, void* stream);
+
+/* Replaces dn_work_bytes (src/cuda/prefill.cuh:41): scratch bytes of qwa_deltanet_rows for B tokens. */
+size_t qwa_dn_work_bytes(int B);
+
+/* Replaces deltanet_rows (src/cuda/prefill.cuh:42-44): B prefill tokens.  qkv [B][10240], z [B][6144], beta / alpha
+ * raw [B][48].  Updates the conv window (read from buffer cin, the window after the B tokens written to buffer
+ * cin ^ 1) and the state.  work: >= qwa_dn_work_bytes(B).  core_out [B][6144] fp32 scratch, written after qkv was
+ * last read (may alias qkv).  o16 [B][6144] fp16 gated-normed output (must not overlap core_out). */
+int qwa_deltanet_rows(const qwa_dn_params* p, const float* qkv, const float* z, const float* beta_raw,
+                      const float* alpha_raw, int B, int cin, float eps, void* work, float* core_out, uint16_t* o16,
+                      void* stream);
 
 /* Opt-in kernel timing (no reference counterpart; the reference times phases with env-gated GPU timers,
  * src/runtime/engine.cpp:2477-2480): between qwa_profile_begin() and qwa_profile_end(), every launch of an

@@ -266,6 +266,71 @@ int qwa_kv_unpack(const void* src, const qwa_kv_layer* kv, int kvt, int n_pos, v
     return kv_move(kv, kvt, n_pos, static_cast<uint8_t*>(const_cast<void*>(src)), false, stream, "kv_unpack");
 }
 
+// ---- Gated DeltaNet
+namespace {
+int check_dn_params(const qwa_dn_params* p, const char* fn) {
+    if (p == nullptr || !p->conv_w || !p->dt_bias || !p->ssm_a || !p->ssm_norm || !p->conv_state || !p->ssm_state)
+        return fail(QWA_ERR_INVALID, "%s: incomplete DeltaNet parameters", fn);
+    return QWA_OK;
+}
+}  // namespace
+
+int qwa_deltanet_multi(const qwa_dn_params* p, int cin, const qwa_dn_tokens* in, int n_commit, int n_new,
+                       int write_after, float eps, float* o, const qwa_act_q8* oq, void* stream) {
+    const char* fn = "deltanet_multi";
+    int st;
+    if ((st = check_dn_params(p, fn))) return st;
+    if (in == nullptr) return fail(QWA_ERR_INVALID, "%s: no token inputs", fn);
+    if (n_commit < 0 || n_new < 0) return fail(QWA_ERR_INVALID, "%s: n_commit %d, n_new %d", fn, n_commit, n_new);
+    if (n_new > QWA_DN_MAXN) return fail(QWA_ERR_RANGE, "%s: %d new tokens > %d", fn, n_new, QWA_DN_MAXN);
+    if (n_commit + n_new == 0) return QWA_OK;  // nothing to apply (the reference returns too)
+    if (cin != 0 && cin != 1) return fail(QWA_ERR_INVALID, "%s: conv buffer %d (0 or 1)", fn, cin);
+    if (write_after < 0 || write_after > n_commit + n_new)
+        return fail(QWA_ERR_RANGE, "%s: write_after %d outside [0, %d]", fn, write_after, n_commit + n_new);
+    if (n_commit > 0 && (!in->sqkv || !in->sbeta || !in->salpha))
+        return fail(QWA_ERR_INVALID, "%s: pending tokens without saved inputs", fn);
+    if (n_new > 0 && (!in->qkv || !in->z || !in->beta || !in->alpha || !o))
+        return fail(QWA_ERR_INVALID, "%s: new tokens without inputs or output", fn);
+    if (n_new > 0 && in->qkv_split < 10240 && (in->qkv_split < 0 || !in->qkv_host || in->qkv_ld < 10240 - in->qkv_split))
+        return fail(QWA_ERR_INVALID, "%s: qkv host part (split %d, ld %d)", fn, in->qkv_split, in->qkv_ld);
+    if (n_new > 0 && in->z_split < 6144 && (in->z_split < 0 || !in->z_host || in->z_ld < 6144 - in->z_split))
+        return fail(QWA_ERR_INVALID, "%s: z host part (split %d, ld %d)", fn, in->z_split, in->z_ld);
+    if ((in->obeta == nullptr) != (in->oalpha == nullptr))
+        return fail(QWA_ERR_INVALID, "%s: obeta and oalpha must be given together", fn);
+    if (oq && (!oq->q || !oq->d || !oq->s)) return fail(QWA_ERR_INVALID, "%s: incomplete ActQ8 output", fn);
+    return from_hip(qwa::launch_dn_multi(*p, cin, *in, n_commit, n_new, write_after, eps, o, oq, as_stream(stream)),
+                    fn);
+}
+
+int qwa_deltanet_step(const qwa_dn_params* p, const float* qkv, const float* z, const float* beta_raw,
+                      const float* alpha_raw, int parity, float eps, float* o, const qwa_act_q8* oq, void* stream) {
+    qwa_dn_tokens in = {};
+    in.qkv = qkv;
+    in.z = z;
+    in.beta = beta_raw;
+    in.alpha = alpha_raw;
+    in.qkv_split = 1 << 30;
+    in.z_split = 1 << 30;
+    return qwa_deltanet_multi(p, parity, &in, 0, 1, 1, eps, o, oq, stream);
+}
+
+size_t qwa_dn_work_bytes(int B) { return B > 0 ? qwa::dn_work_bytes(B) : 0; }
+
+int qwa_deltanet_rows(const qwa_dn_params* p, const float* qkv, const float* z, const float* beta_raw,
+                      const float* alpha_raw, int B, int cin, float eps, void* work, float* core_out, uint16_t* o16,
+                      void* stream) {
+    const char* fn = "deltanet_rows";
+    int st;
+    if ((st = check_dn_params(p, fn))) return st;
+    if (B <= 0 || B > 65535) return fail(QWA_ERR_RANGE, "%s: B = %d", fn, B);
+    if (cin != 0 && cin != 1) return fail(QWA_ERR_INVALID, "%s: conv buffer %d (0 or 1)", fn, cin);
+    if (!qkv || !z || !beta_raw || !alpha_raw || !work || !core_out || !o16)
+        return fail(QWA_ERR_INVALID, "%s: missing buffer", fn);
+    return from_hip(qwa::launch_dn_rows(*p, qkv, z, beta_raw, alpha_raw, B, cin, eps, work, core_out, o16,
+                                        as_stream(stream)),
+                    fn);
+}
+
 int qwa_profile_begin(void) {
     const size_t bytes = (size_t)PROF_MAX * qwa::PROF_MAX_WG * 2 * sizeof(unsigned long long);
     if (g_prof.stamps == nullptr) {

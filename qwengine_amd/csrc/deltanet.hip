@@ -1,0 +1,414 @@
+// Gated DeltaNet token mixer (gfx950): the recurrent layers that sit between the gated-attention layers.
+//
+// Per token and value head h (key head h % 16): causal depthwise conv (width 4) + SiLU over the q | k | v channels,
+// L2-normalised q and k, beta = sigmoid(b), decay = exp(softplus(a + dt_bias) * A), then the gated delta rule on the
+// 128 x 128 state S (column j = value dim, row i = key dim):
+//     S <- decay S;  kv = S^T k;  S <- S + k ((v - kv) beta)^T;  o = S^T q / sqrt(128)
+// and the gated RMSNorm rmsnorm(o) * ssm_norm * silu(z).  Semantics: src/reference/ref_model.cpp:169-256 (CPU, FP32);
+// entry points and state conventions: src/cuda/ops.cuh:54-97 (decode, lazy commit), src/cuda/prefill.cuh:37-44
+// (prefill rows).
+//
+// Decode / verify (k_dn_multi): one workgroup of 8 waves per value head (48 workgroups).  The head's state stays in
+// registers for the whole call: lane (column 16 w + l / 4, row group l % 4) of wave w holds the 32 rows
+// 32 (l % 4) .. + 31 of its column, so both dot products per column reduce over 4 lanes (two quad-permute adds).
+// Tokens are applied one after the other with the same code, so a token sequence gives the same bits however it is
+// split into calls (the lazy-commit contract, src/cuda/ops.cuh:93-95).
+//
+// Prefill (B tokens): token-parallel conv, conv-window and q/k-normalisation kernels, the sequential recurrence over
+// (48 heads x 4 groups of 32 columns) with the tokens' q / k / v staged in LDS, and the gated norm to fp16.
+#include <type_traits>
+
+#include "launch.hpp"
+#include "qwattn_common.hpp"
+
+namespace qwa {
+
+constexpr int DN_CH = 10240;  // conv channels: q (16 x 128) | k (16 x 128) | v (48 x 128)
+constexpr int DN_QK = 2048;
+constexpr int DN_HD = 128;
+constexpr int DN_KH = 16;
+constexpr int DN_VH = 48;
+constexpr int DN_VD = DN_VH * DN_HD;  // 6144
+constexpr int DN_BA_LD = 64;          // row stride of the decode path's beta / alpha inputs
+constexpr int DN_KPAD = DN_HD + 16;   // padded q / k row in LDS: element i at i + 4 (i / 32)
+
+__device__ __forceinline__ float dn_silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ int dn_pad(int i) { return i + 4 * (i >> 5); }
+
+// sum over the 4 lanes of a quad (the 4 row groups of one state column)
+__device__ __forceinline__ float quad_sum(float x) {
+    x += __shfl_xor(x, 1, 64);
+    return x + __shfl_xor(x, 2, 64);
+}
+
+// ------------------------------------------------------------------------------------------------------- decode
+__global__ void __launch_bounds__(512) k_dn_multi(qwa_dn_params p, int cin, qwa_dn_tokens in, int n_commit,
+                                                  int n_new, int write_after, float eps, float* __restrict__ o,
+                                                  qwa_act_q8 oq, int do_q) {
+    const int h = blockIdx.x, kh = h % DN_KH, t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63;
+    __shared__ __attribute__((aligned(16))) float s_q[DN_KPAD], s_k[DN_KPAD];
+    __shared__ float s_v[DN_HD], s_o[DN_HD], s_misc[4], s_red[2];
+    __shared__ float s_xc[QWA_DN_MAXN][3 * DN_HD], s_z[QWA_DN_MAXN][DN_HD];
+    const float* cs_in = p.conv_state + (size_t)cin * 3 * DN_CH;
+    float* cs_out = p.conv_state + (size_t)(cin ^ 1) * 3 * DN_CH;
+
+    // conv channel of this thread: q and k of key head kh, v of value head h
+    int c = 0;
+    float x0 = 0.0f, x1 = 0.0f, x2 = 0.0f;
+    float4 w = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (t < 3 * DN_HD) {
+        c = t < DN_HD ? kh * DN_HD + t : t < 2 * DN_HD ? DN_QK + kh * DN_HD + (t - DN_HD) : 2 * DN_QK + h * DN_HD + (t - 2 * DN_HD);
+        x0 = cs_in[c];
+        x1 = cs_in[DN_CH + c];
+        x2 = cs_in[2 * DN_CH + c];
+        w = *reinterpret_cast<const float4*>(p.conv_w + (size_t)c * 4);
+    }
+    // the q / k channels are shared by value heads kh, kh + 16, kh + 32: only the first writes them back
+    const bool owner = t < 3 * DN_HD && (t >= 2 * DN_HD || h < DN_KH);
+    // the new tokens' conv and gate inputs, read once up front (part of them may live in mapped host memory)
+    if (t < 3 * DN_HD) {
+        for (int ni = 0; ni < n_new; ni++)
+            s_xc[ni][t] = c >= in.qkv_split ? in.qkv_host[(size_t)ni * in.qkv_ld + (c - in.qkv_split)]
+                                            : in.qkv[(size_t)ni * DN_CH + c];
+    } else {
+        const int j = t - 3 * DN_HD, zi = h * DN_HD + j;
+        for (int ni = 0; ni < n_new; ni++)
+            s_z[ni][j] = zi >= in.z_split ? in.z_host[(size_t)ni * in.z_ld + (zi - in.z_split)]
+                                          : in.z[(size_t)ni * DN_VD + zi];
+    }
+
+    // this lane's 32 state values: column j, rows 32 g .. 32 g + 31 (global layout [h][j][i])
+    const int j = 16 * wave + (lane >> 2), g = lane & 3;
+    float* Sh = p.ssm_state + (size_t)h * DN_HD * DN_HD;
+    float s[32];
+    {
+        const float4* src = reinterpret_cast<const float4*>(Sh + (size_t)j * DN_HD + 32 * g);
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const float4 v = src[r];
+            s[4 * r] = v.x; s[4 * r + 1] = v.y; s[4 * r + 2] = v.z; s[4 * r + 3] = v.w;
+        }
+    }
+    const float oscale = 1.0f / sqrtf((float)DN_HD);
+    __syncthreads();
+
+    const int ntot = n_commit + n_new;
+    for (int i = 0; i < ntot; i++) {
+        const bool is_new = i >= n_commit;
+        const int ni = i - n_commit;
+        const float* beta_raw = is_new ? in.beta + ni * DN_BA_LD : in.sbeta + i * DN_BA_LD;
+        const float* alpha_raw = is_new ? in.alpha + ni * DN_BA_LD : in.salpha + i * DN_BA_LD;
+        // 1) causal conv + SiLU (pending tokens replay their saved inputs)
+        if (t < 3 * DN_HD) {
+            const float xc = is_new ? s_xc[ni][t] : in.sqkv[(size_t)i * DN_CH + c];
+            const float val = dn_silu(w.x * x0 + w.y * x1 + w.z * x2 + w.w * xc);
+            if (t < DN_HD) s_q[dn_pad(t)] = val;
+            else if (t < 2 * DN_HD) s_k[dn_pad(t - DN_HD)] = val;
+            else s_v[t - 2 * DN_HD] = val;
+            x0 = x1;
+            x1 = x2;
+            x2 = xc;
+            if (owner) {
+                if (is_new && in.oqkv) in.oqkv[(size_t)ni * DN_CH + c] = xc;
+                if (i == write_after - 1) {  // the window at the commit point, to the other buffer
+                    cs_out[c] = x0;
+                    cs_out[DN_CH + c] = x1;
+                    cs_out[2 * DN_CH + c] = x2;
+                }
+            }
+        }
+        if (is_new && in.obeta && t == 0) {
+            in.obeta[ni * DN_BA_LD + h] = beta_raw[h];
+            in.oalpha[ni * DN_BA_LD + h] = alpha_raw[h];
+        }
+        __syncthreads();
+        // 2) L2 norms of q (wave 0) and k (wave 1); beta and decay (wave 2)
+        if (wave < 2) {
+            const float* src = wave == 0 ? s_q : s_k;
+            const float a0 = src[dn_pad(lane)], a1 = src[dn_pad(lane + 64)];
+            const float sum = wave_sum(a0 * a0 + a1 * a1);
+            if (lane == 0) s_misc[wave] = 1.0f / fmaxf(sqrtf(sum), eps);
+        } else if (wave == 2 && lane == 0) {
+            const float a = alpha_raw[h] + p.dt_bias[h];
+            const float sp = a > 20.0f ? a : logf(1.0f + expf(a));
+            s_misc[2] = 1.0f / (1.0f + expf(-beta_raw[h]));
+            s_misc[3] = expf(sp * p.ssm_a[h]);
+        }
+        __syncthreads();
+        // 3) the gated delta rule on this lane's 32 state values
+        const float qs = s_misc[0], ks = s_misc[1], beta = s_misc[2], decay = s_misc[3];
+        float kr[32], qr[32];
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const float4 k4 = *reinterpret_cast<const float4*>(&s_k[36 * g + 4 * r]);
+            const float4 q4 = *reinterpret_cast<const float4*>(&s_q[36 * g + 4 * r]);
+            kr[4 * r] = k4.x * ks; kr[4 * r + 1] = k4.y * ks; kr[4 * r + 2] = k4.z * ks; kr[4 * r + 3] = k4.w * ks;
+            qr[4 * r] = q4.x * qs; qr[4 * r + 1] = q4.y * qs; qr[4 * r + 2] = q4.z * qs; qr[4 * r + 3] = q4.w * qs;
+        }
+        float ka = 0.0f, kb = 0.0f, kc = 0.0f, kd = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            s[4 * r] *= decay; s[4 * r + 1] *= decay; s[4 * r + 2] *= decay; s[4 * r + 3] *= decay;
+            ka = fmaf(s[4 * r], kr[4 * r], ka);
+            kb = fmaf(s[4 * r + 1], kr[4 * r + 1], kb);
+            kc = fmaf(s[4 * r + 2], kr[4 * r + 2], kc);
+            kd = fmaf(s[4 * r + 3], kr[4 * r + 3], kd);
+        }
+        const float kv = quad_sum((ka + kb) + (kc + kd));  // (S^T k)_j over the column's 128 rows
+        const float delta = (s_v[j] - kv) * beta;
+        float oa = 0.0f, ob = 0.0f, oc = 0.0f, od = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            s[4 * r] = fmaf(kr[4 * r], delta, s[4 * r]);
+            s[4 * r + 1] = fmaf(kr[4 * r + 1], delta, s[4 * r + 1]);
+            s[4 * r + 2] = fmaf(kr[4 * r + 2], delta, s[4 * r + 2]);
+            s[4 * r + 3] = fmaf(kr[4 * r + 3], delta, s[4 * r + 3]);
+            oa = fmaf(s[4 * r], qr[4 * r], oa);
+            ob = fmaf(s[4 * r + 1], qr[4 * r + 1], ob);
+            oc = fmaf(s[4 * r + 2], qr[4 * r + 2], oc);
+            od = fmaf(s[4 * r + 3], qr[4 * r + 3], od);
+        }
+        const float oj = quad_sum((oa + ob) + (oc + od));
+        if (is_new && g == 0) s_o[j] = oj * oscale;
+        if (i == write_after - 1) {  // the state at the commit point, in place
+            float4* dst = reinterpret_cast<float4*>(Sh + (size_t)j * DN_HD + 32 * g);
+#pragma unroll
+            for (int r = 0; r < 8; r++) dst[r] = make_float4(s[4 * r], s[4 * r + 1], s[4 * r + 2], s[4 * r + 3]);
+        }
+        // 4) new tokens: gated RMSNorm rmsnorm(o) * ssm_norm * silu(z), optional ActQ8 and mapped-host copy
+        if (is_new) {
+            __syncthreads();
+            if (wave < 2) {
+                const float v = s_o[t];
+                const float sum = wave_sum(v * v);
+                if (lane == 0) s_red[wave] = sum;
+            }
+            __syncthreads();
+            if (wave < 2) {
+                const float rs = 1.0f / sqrtf((s_red[0] + s_red[1]) / DN_HD + eps);
+                const float v = s_o[t] * rs * p.ssm_norm[t] * dn_silu(s_z[ni][t]);
+                const size_t oi = (size_t)ni * DN_VD + h * DN_HD + t;
+                o[oi] = v;
+                if (in.o_host) in.o_host[oi] = v;
+                if (do_q) {
+                    // ActQ8 (src/cuda/common.cuh:188-197) per 32 outputs: d = amax / 127, q = rint(v / d), s = d sum(q)
+                    const float amax = half_max(fabsf(v));
+                    const float db = amax / 127.0f;
+                    const int qi = db > 0.0f ? (int)__builtin_rintf(v / db) : 0;
+                    oq.q[oi] = (int8_t)qi;
+                    const float qsum = half_sum((float)qi);
+                    if ((lane & 31) == 0) {
+                        const size_t blk = (size_t)ni * (DN_VD / 32) + h * 4 + (t >> 5);
+                        oq.d[blk] = db;
+                        oq.s[blk] = db * qsum;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (in.o_host) __threadfence_system();
+}
+
+// ------------------------------------------------------------------------------------------------------ prefill
+struct DnRows {
+    float* conv;   // [B][10240] after SiLU
+    float* qn;     // [B][2048] L2-normalised q
+    float* kn;     // [B][2048] L2-normalised k
+    float* beta;   // [B][48]
+    float* decay;  // [B][48]
+};
+
+__host__ __device__ inline DnRows dn_rows_split(void* work, int B) {
+    float* f = static_cast<float*>(work);
+    DnRows r;
+    r.conv = f;
+    f += (size_t)B * DN_CH;
+    r.qn = f;
+    f += (size_t)B * DN_QK;
+    r.kn = f;
+    f += (size_t)B * DN_QK;
+    r.beta = f;
+    f += (size_t)B * DN_VH;
+    r.decay = f;
+    return r;
+}
+
+size_t dn_work_bytes(int B) { return (size_t)B * (DN_CH + 2 * DN_QK + 2 * DN_VH) * sizeof(float); }
+
+// out[t][c] = silu(sum_k w[c][k] in(t - 3 + k)), in(i) = qkv[i][c] for i >= 0, else row 3 + i of the old window
+__global__ void __launch_bounds__(256) k_dn_conv_rows(const float* __restrict__ qkv, const float* __restrict__ cs_old,
+                                                      const float* __restrict__ conv_w, float* __restrict__ out) {
+    const int t = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= DN_CH) return;
+    const float4 w = *reinterpret_cast<const float4*>(conv_w + (size_t)c * 4);
+    float x[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = t - 3 + k;
+        x[k] = i >= 0 ? qkv[(size_t)i * DN_CH + c] : cs_old[(size_t)(3 + i) * DN_CH + c];
+    }
+    out[(size_t)t * DN_CH + c] = dn_silu(w.x * x[0] + w.y * x[1] + w.z * x[2] + w.w * x[3]);
+}
+
+// the window after the B tokens (rows k = input B - 3 + k), into the other buffer
+__global__ void __launch_bounds__(256) k_dn_conv_state(const float* __restrict__ qkv, const float* __restrict__ cs_old,
+                                                       int B, float* __restrict__ cs_new) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= DN_CH) return;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const int i = B - 3 + k;
+        cs_new[(size_t)k * DN_CH + c] = i >= 0 ? qkv[(size_t)i * DN_CH + c] : cs_old[(size_t)(3 + i) * DN_CH + c];
+    }
+}
+
+// per token: L2-normalised q and k of the 16 key heads (wave w: heads w, w + 4, ... of q then k), beta and decay
+__global__ void __launch_bounds__(256) k_dn_prep_rows(DnRows r, const float* __restrict__ beta_raw,
+                                                      const float* __restrict__ alpha_raw,
+                                                      const float* __restrict__ dt_bias,
+                                                      const float* __restrict__ ssm_a, float eps) {
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int jn = wave; jn < 2 * DN_KH; jn += 4) {
+        const bool is_k = jn >= DN_KH;
+        const int kh = jn % DN_KH;
+        const float* src = r.conv + (size_t)t * DN_CH + (is_k ? DN_QK : 0) + kh * DN_HD;
+        const float a0 = src[lane], a1 = src[lane + 64];
+        const float inv = 1.0f / fmaxf(sqrtf(wave_sum(a0 * a0 + a1 * a1)), eps);
+        float* dst = (is_k ? r.kn : r.qn) + (size_t)t * DN_QK + kh * DN_HD;
+        dst[lane] = a0 * inv;
+        dst[lane + 64] = a1 * inv;
+    }
+    if (threadIdx.x < DN_VH) {
+        const int h = threadIdx.x;
+        const float a = alpha_raw[(size_t)t * DN_VH + h] + dt_bias[h];
+        const float sp = a > 20.0f ? a : logf(1.0f + expf(a));
+        r.beta[(size_t)t * DN_VH + h] = 1.0f / (1.0f + expf(-beta_raw[(size_t)t * DN_VH + h]));
+        r.decay[(size_t)t * DN_VH + h] = expf(sp * ssm_a[h]);
+    }
+}
+
+// The recurrence over B tokens: grid (48 heads, 4 groups of 32 columns), 2 waves; lane (column 16 w + l / 4 of the
+// group, row group l % 4) holds 32 rows of its column for the whole call.  DN_RT tokens at a time are staged in LDS
+// (q / k rows padded so that the 4 row groups read different banks).  core_out may alias qkv: it is written only
+// after the conv kernel has read qkv.
+constexpr int DN_RT = 16;
+constexpr int DN_RCOL = 32;
+__global__ void __launch_bounds__(128) k_dn_recur_rows(DnRows r, float* __restrict__ state, int B,
+                                                       float* __restrict__ core_out) {
+    const int h = blockIdx.x, cgp = blockIdx.y, kh = h % DN_KH;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane & 3;
+    const int jc = 16 * wave + (lane >> 2), col = cgp * DN_RCOL + jc;
+    __shared__ __attribute__((aligned(16))) float sk[DN_RT][DN_KPAD], sq[DN_RT][DN_KPAD];
+    __shared__ float sv[DN_RT][DN_RCOL], so[DN_RT][DN_RCOL], sbeta[DN_RT], sdecay[DN_RT];
+    float* Sh = state + (size_t)h * DN_HD * DN_HD;
+    float s[32];
+    {
+        const float4* src = reinterpret_cast<const float4*>(Sh + (size_t)col * DN_HD + 32 * g);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = src[i];
+            s[4 * i] = v.x; s[4 * i + 1] = v.y; s[4 * i + 2] = v.z; s[4 * i + 3] = v.w;
+        }
+    }
+    const float oscale = 1.0f / sqrtf((float)DN_HD);
+    for (int t0 = 0; t0 < B; t0 += DN_RT) {
+        const int nt = min(DN_RT, B - t0);
+        __syncthreads();  // the previous group's outputs are written out
+        for (int i = threadIdx.x; i < nt * DN_HD; i += 128) {
+            const int tt = i / DN_HD, e = i % DN_HD;
+            sk[tt][dn_pad(e)] = r.kn[(size_t)(t0 + tt) * DN_QK + kh * DN_HD + e];
+            sq[tt][dn_pad(e)] = r.qn[(size_t)(t0 + tt) * DN_QK + kh * DN_HD + e];
+        }
+        for (int i = threadIdx.x; i < nt * DN_RCOL; i += 128) {
+            const int tt = i / DN_RCOL, e = i % DN_RCOL;
+            sv[tt][e] = r.conv[(size_t)(t0 + tt) * DN_CH + 2 * DN_QK + h * DN_HD + cgp * DN_RCOL + e];
+        }
+        if (threadIdx.x < nt) {
+            sbeta[threadIdx.x] = r.beta[(size_t)(t0 + threadIdx.x) * DN_VH + h];
+            sdecay[threadIdx.x] = r.decay[(size_t)(t0 + threadIdx.x) * DN_VH + h];
+        }
+        __syncthreads();
+        for (int tt = 0; tt < nt; tt++) {
+            const float4* kp = reinterpret_cast<const float4*>(&sk[tt][36 * g]);
+            const float4* qp = reinterpret_cast<const float4*>(&sq[tt][36 * g]);
+            const float decay = sdecay[tt], beta = sbeta[tt];
+            float ka = 0.0f, kb = 0.0f, kc = 0.0f, kd = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 k4 = kp[i];
+                s[4 * i] *= decay; s[4 * i + 1] *= decay; s[4 * i + 2] *= decay; s[4 * i + 3] *= decay;
+                ka = fmaf(s[4 * i], k4.x, ka);
+                kb = fmaf(s[4 * i + 1], k4.y, kb);
+                kc = fmaf(s[4 * i + 2], k4.z, kc);
+                kd = fmaf(s[4 * i + 3], k4.w, kd);
+            }
+            const float kv = quad_sum((ka + kb) + (kc + kd));
+            const float delta = (sv[tt][jc] - kv) * beta;
+            float oa = 0.0f, ob = 0.0f, oc = 0.0f, od = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 k4 = kp[i], q4 = qp[i];
+                s[4 * i] = fmaf(k4.x, delta, s[4 * i]);
+                s[4 * i + 1] = fmaf(k4.y, delta, s[4 * i + 1]);
+                s[4 * i + 2] = fmaf(k4.z, delta, s[4 * i + 2]);
+                s[4 * i + 3] = fmaf(k4.w, delta, s[4 * i + 3]);
+                oa = fmaf(s[4 * i], q4.x, oa);
+                ob = fmaf(s[4 * i + 1], q4.y, ob);
+                oc = fmaf(s[4 * i + 2], q4.z, oc);
+                od = fmaf(s[4 * i + 3], q4.w, od);
+            }
+            const float ov = quad_sum((oa + ob) + (oc + od));
+            if (g == 0) so[tt][jc] = ov * oscale;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < nt * DN_RCOL; i += 128) {
+            const int tt = i / DN_RCOL, e = i % DN_RCOL;
+            core_out[(size_t)(t0 + tt) * DN_VD + h * DN_HD + cgp * DN_RCOL + e] = so[tt][e];
+        }
+    }
+    float4* dst = reinterpret_cast<float4*>(Sh + (size_t)col * DN_HD + 32 * g);
+#pragma unroll
+    for (int i = 0; i < 8; i++) dst[i] = make_float4(s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]);
+}
+
+// gated RMSNorm per (token, value head), fp16 out: grid (B, 48), 128 threads
+__global__ void __launch_bounds__(128) k_dn_gnorm_rows(const float* __restrict__ core, const float* __restrict__ z,
+                                                       const float* __restrict__ nw, float eps,
+                                                       uint16_t* __restrict__ o16) {
+    __shared__ float red[2];
+    const int t = blockIdx.x, h = blockIdx.y, j = threadIdx.x, wave = j >> 6;
+    const size_t idx = (size_t)t * DN_VD + h * DN_HD + j;
+    const float v = core[idx];
+    const float sum = wave_sum(v * v);
+    if ((j & 63) == 0) red[wave] = sum;
+    __syncthreads();
+    const float rs = 1.0f / sqrtf((red[0] + red[1]) / DN_HD + eps);
+    o16[idx] = f2h_bits(v * rs * nw[j] * dn_silu(z[idx]));
+}
+
+// ------------------------------------------------------------------------------------------------------ launchers
+hipError_t launch_dn_multi(const qwa_dn_params& p, int cin, const qwa_dn_tokens& in, int n_commit, int n_new,
+                           int write_after, float eps, float* o, const qwa_act_q8* oq, hipStream_t st) {
+    const qwa_act_q8 a = oq ? *oq : qwa_act_q8{nullptr, nullptr, nullptr};
+    hipLaunchKernelGGL(k_dn_multi, dim3(DN_VH), dim3(512), 0, st, p, cin, in, n_commit, n_new, write_after, eps, o,
+                       a, oq != nullptr ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_dn_rows(const qwa_dn_params& p, const float* qkv, const float* z, const float* beta_raw,
+                          const float* alpha_raw, int B, int cin, float eps, void* work, float* core_out,
+                          uint16_t* o16, hipStream_t st) {
+    const DnRows r = dn_rows_split(work, B);
+    const float* cs_old = p.conv_state + (size_t)cin * 3 * DN_CH;
+    float* cs_new = p.conv_state + (size_t)(cin ^ 1) * 3 * DN_CH;
+    hipLaunchKernelGGL(k_dn_conv_rows, dim3(DN_CH / 256, B), dim3(256), 0, st, qkv, cs_old, p.conv_w, r.conv);
+    hipLaunchKernelGGL(k_dn_conv_state, dim3(DN_CH / 256), dim3(256), 0, st, qkv, cs_old, B, cs_new);
+    hipLaunchKernelGGL(k_dn_prep_rows, dim3(B), dim3(256), 0, st, r, beta_raw, alpha_raw, p.dt_bias, p.ssm_a, eps);
+    hipLaunchKernelGGL(k_dn_recur_rows, dim3(DN_VH, DN_HD / DN_RCOL), dim3(128), 0, st, r, p.ssm_state, B, core_out);
+    hipLaunchKernelGGL(k_dn_gnorm_rows, dim3(B, DN_VH), dim3(128), 0, st, core_out, z, p.ssm_norm, eps, o16);
+    return hipGetLastError();
+}
+
+}  // namespace qwa

@@ -47,6 +47,14 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
 hipError_t launch_decode_simple(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int n_pos,
                                 float* out, const qwa_act_q8* oq, hipStream_t st);
 
+// Gated DeltaNet (deltanet.hip)
+size_t dn_work_bytes(int B);
+hipError_t launch_dn_multi(const qwa_dn_params& p, int cin, const qwa_dn_tokens& in, int n_commit, int n_new,
+                           int write_after, float eps, float* o, const qwa_act_q8* oq, hipStream_t st);
+hipError_t launch_dn_rows(const qwa_dn_params& p, const float* qkv, const float* z, const float* beta_raw,
+                          const float* alpha_raw, int B, int cin, float eps, void* work, float* core_out,
+                          uint16_t* o16, hipStream_t st);
+
 hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
                           uint16_t* out16, hipStream_t st);
 hipError_t launch_prefill_simple(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,

@@ -41,6 +41,20 @@ class _RowSrcC(ctypes.Structure):
     _fields_ = [("dev", ctypes.c_void_p), ("host", ctypes.c_void_p), ("split", ctypes.c_int), ("host_ld", ctypes.c_int)]
 
 
+class _DNParamsC(ctypes.Structure):
+    _fields_ = [("conv_w", ctypes.c_void_p), ("dt_bias", ctypes.c_void_p), ("ssm_a", ctypes.c_void_p),
+                ("ssm_norm", ctypes.c_void_p), ("conv_state", ctypes.c_void_p), ("ssm_state", ctypes.c_void_p)]
+
+
+class _DNTokensC(ctypes.Structure):
+    _fields_ = [("sqkv", ctypes.c_void_p), ("sbeta", ctypes.c_void_p), ("salpha", ctypes.c_void_p),
+                ("qkv", ctypes.c_void_p), ("z", ctypes.c_void_p), ("beta", ctypes.c_void_p), ("alpha", ctypes.c_void_p),
+                ("oqkv", ctypes.c_void_p), ("obeta", ctypes.c_void_p), ("oalpha", ctypes.c_void_p),
+                ("qkv_host", ctypes.c_void_p), ("qkv_split", ctypes.c_int), ("qkv_ld", ctypes.c_int),
+                ("z_host", ctypes.c_void_p), ("z_split", ctypes.c_int), ("z_ld", ctypes.c_int),
+                ("o_host", ctypes.c_void_p)]
+
+
 EXPORTS = {
     # name: (restype, argtypes)
     "qwa_kv_value_bytes": (ctypes.c_size_t, [ctypes.c_int]),
@@ -78,6 +92,14 @@ EXPORTS = {
                                    ctypes.c_void_p]),
     "qwa_kv_unpack": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(_KVLayerC), ctypes.c_int, ctypes.c_int,
                                      ctypes.c_void_p]),
+    "qwa_deltanet_step": (ctypes.c_int, [ctypes.POINTER(_DNParamsC)] + [ctypes.c_void_p] * 4 +
+                          [ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.POINTER(_ActQ8C), ctypes.c_void_p]),
+    "qwa_deltanet_multi": (ctypes.c_int, [ctypes.POINTER(_DNParamsC), ctypes.c_int, ctypes.POINTER(_DNTokensC)] +
+                           [ctypes.c_int] * 3 + [ctypes.c_float, ctypes.c_void_p, ctypes.POINTER(_ActQ8C),
+                                                 ctypes.c_void_p]),
+    "qwa_dn_work_bytes": (ctypes.c_size_t, [ctypes.c_int]),
+    "qwa_deltanet_rows": (ctypes.c_int, [ctypes.POINTER(_DNParamsC)] + [ctypes.c_void_p] * 4 +
+                          [ctypes.c_int, ctypes.c_int, ctypes.c_float] + [ctypes.c_void_p] * 4),
     "qwa_profile_begin": (ctypes.c_int, []),
     "qwa_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
     "qwa_profile_device_ms": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double)]),
@@ -328,3 +350,80 @@ def kv_unpack(src, kv: KVLayer, kvt, n_pos: int, stream=None) -> None:
 def kv_append(xk, xv, pos0: int, n: int, kvt, kv: KVLayer, stream=None) -> None:
     """Quantize-on-append of raw K/V rows [n, 4, 256] (the row store of src/cuda/common.cuh:199-228)."""
     _check(lib().qwa_kv_append(_ptr(xk), _ptr(xv), pos0, n, _kvt(kvt), ctypes.byref(kv.c()), _stream(stream)))
+
+
+# ---- Gated DeltaNet ------------------------------------------------------------------------------------------------
+DN_CH, DN_QK, DN_VD, DN_VH, DN_KH, DN_HD, DN_MAXN = 10240, 2048, 6144, 48, 16, 128, 7
+
+
+@dataclass
+class DNParams:
+    """One Gated DeltaNet layer (mirror of q38rt::cuda::DeltaNetParams, src/cuda/ops.cuh:54-62).
+
+    conv_w [10240][4], dt_bias / ssm_a [48], ssm_norm [128] fp32; conv_state [2][3][10240] (ping-pong buffers);
+    ssm_state [48][128 col j][128 row i] fp32."""
+    conv_w: torch.Tensor
+    dt_bias: torch.Tensor
+    ssm_a: torch.Tensor
+    ssm_norm: torch.Tensor
+    conv_state: torch.Tensor
+    ssm_state: torch.Tensor
+
+    def c(self) -> _DNParamsC:
+        return _DNParamsC(_ptr(self.conv_w), _ptr(self.dt_bias), _ptr(self.ssm_a), _ptr(self.ssm_norm),
+                          _ptr(self.conv_state), _ptr(self.ssm_state))
+
+
+@dataclass
+class DNTokens:
+    """Token inputs of deltanet_multi (mirror of q38rt::cuda::DNTokens, src/cuda/ops.cuh:74-91).  Host parts:
+    qkv channels >= qkv_split come from qkv_host [n][qkv_ld], z channels >= z_split from z_host [n][z_ld]."""
+    sqkv: object = None
+    sbeta: object = None
+    salpha: object = None
+    qkv: object = None
+    z: object = None
+    beta: object = None
+    alpha: object = None
+    oqkv: object = None
+    obeta: object = None
+    oalpha: object = None
+    qkv_host: object = None
+    qkv_split: int = 1 << 30
+    qkv_ld: int = 0
+    z_host: object = None
+    z_split: int = 1 << 30
+    z_ld: int = 0
+    o_host: object = None
+
+    def c(self) -> _DNTokensC:
+        return _DNTokensC(_ptr(self.sqkv), _ptr(self.sbeta), _ptr(self.salpha), _ptr(self.qkv), _ptr(self.z),
+                          _ptr(self.beta), _ptr(self.alpha), _ptr(self.oqkv), _ptr(self.obeta), _ptr(self.oalpha),
+                          _ptr(self.qkv_host), self.qkv_split, self.qkv_ld, _ptr(self.z_host), self.z_split,
+                          self.z_ld, _ptr(self.o_host))
+
+
+def deltanet_step(p: DNParams, qkv, z, beta_raw, alpha_raw, parity: int, eps: float, o, oq: ActQ8 | None = None,
+                  stream=None) -> None:
+    """src/cuda/ops.cuh:67-68."""
+    _check(lib().qwa_deltanet_step(ctypes.byref(p.c()), _ptr(qkv), _ptr(z), _ptr(beta_raw), _ptr(alpha_raw), parity,
+                                   eps, _ptr(o), _act(oq), _stream(stream)))
+
+
+def deltanet_multi(p: DNParams, cin: int, tokens: DNTokens, n_commit: int, n_new: int, write_after: int, eps: float,
+                   o, oq: ActQ8 | None = None, stream=None) -> None:
+    """src/cuda/ops.cuh:96-97."""
+    _check(lib().qwa_deltanet_multi(ctypes.byref(p.c()), cin, ctypes.byref(tokens.c()), n_commit, n_new,
+                                    write_after, eps, _ptr(o), _act(oq), _stream(stream)))
+
+
+def dn_work_bytes(B: int) -> int:
+    """src/cuda/prefill.cuh:41."""
+    return int(lib().qwa_dn_work_bytes(B))
+
+
+def deltanet_rows(p: DNParams, qkv, z, beta_raw, alpha_raw, B: int, cin: int, eps: float, work, core_out, o16,
+                  stream=None) -> None:
+    """src/cuda/prefill.cuh:42-44."""
+    _check(lib().qwa_deltanet_rows(ctypes.byref(p.c()), _ptr(qkv), _ptr(z), _ptr(beta_raw), _ptr(alpha_raw), B, cin,
+                                   eps, _ptr(work), _ptr(core_out), _ptr(o16), _stream(stream)))

@@ -117,7 +117,15 @@ int main() {
                hipStream_t, float*) = attn_decode_multi;
     void (*pp)(const float*, const float*, const KVLayer&, KVType, int, int, uint16_t*, hipStream_t) = attn_prefill;
     void (*ph)(const float*, const float*, const KVLayer&, KVType, int, int, __half*, hipStream_t) = attn_prefill;
-    return (fp && pp && ph) ? 0 : 3;
+    void (*ds)(const DeltaNetParams&, const float*, const float*, const float*, const float*, int, float, float*,
+               const ActQ8*, hipStream_t) = deltanet_step;
+    void (*dm)(const DeltaNetParams&, int, const DNTokens&, int, int, int, float, float*, const ActQ8*,
+               hipStream_t) = deltanet_multi;
+    void (*dr)(const DeltaNetParams&, const float*, const float*, const float*, const float*, int, int, float, void*,
+               float*, __half*, hipStream_t) = deltanet_rows;
+    DNTokens tk;
+    if (dn_work_bytes(1024) != (size_t)1024 * (10240 + 2 * 2048 + 2 * 48) * 4 || tk.qkv_split != (1 << 30)) return 4;
+    return (fp && pp && ph && ds && dm && dr) ? 0 : 3;
 }
 '''
     tmp = os.path.join(ROOT, "_build_test_shim")
@@ -132,3 +140,31 @@ int main() {
     assert r.returncode == 0, r.stderr[-3000:]
     r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, (r.returncode, r.stderr[-2000:])
+
+
+def _dnp():
+    return ops.DNParams(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000)
+
+
+def test_deltanet_rejects_bad_arguments():
+    """The reference aborts on more than DN_MAXN new tokens (src/cuda/ops.cu:959); the C ABI returns a status."""
+    p = _dnp()
+    tok = ops.DNTokens(qkv=0x1000, z=0x1000, beta=0x1000, alpha=0x1000)
+    with pytest.raises(ops.QwaError, match="new tokens > 7"):
+        ops.deltanet_multi(p, 0, tok, 0, 8, 8, 1e-6, 0x1000)
+    with pytest.raises(ops.QwaError, match="conv buffer"):
+        ops.deltanet_multi(p, 2, tok, 0, 1, 1, 1e-6, 0x1000)
+    with pytest.raises(ops.QwaError, match="write_after"):
+        ops.deltanet_multi(p, 0, tok, 0, 2, 3, 1e-6, 0x1000)
+    with pytest.raises(ops.QwaError, match="saved inputs"):
+        ops.deltanet_multi(p, 0, tok, 1, 1, 2, 1e-6, 0x1000)
+    with pytest.raises(ops.QwaError, match="host part"):
+        ops.deltanet_multi(p, 0, ops.DNTokens(qkv=0x1000, z=0x1000, beta=0x1000, alpha=0x1000, qkv_split=100), 0, 1,
+                           1, 1e-6, 0x1000)
+    with pytest.raises(ops.QwaError, match="incomplete DeltaNet parameters"):
+        ops.deltanet_step(ops.DNParams(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, None), 0x1000, 0x1000, 0x1000,
+                          0x1000, 0, 1e-6, 0x1000)
+    with pytest.raises(ops.QwaError, match="B = 0"):
+        ops.deltanet_rows(p, 0x1000, 0x1000, 0x1000, 0x1000, 0, 0, 1e-6, 0x1000, 0x1000, 0x1000)
+    # nothing to apply is not an error (the reference returns)
+    ops.deltanet_multi(p, 0, ops.DNTokens(), 0, 0, 0, 1e-6, None)
