@@ -74,6 +74,23 @@ def time_calls(torch, fn, reps, warmup):
     return e0.elapsed_time(e1) / reps  # ms
 
 
+def time_graph(torch, fn, reps, warmup=3):
+    """fn captured once into a HIP graph (as the engine runs its decode step), then timed over graph replays: the
+    figure is the GPU's, not the Python launch loop's."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    ms = time_calls(torch, g.replay, reps, warmup)
+    del g
+    return ms
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -206,11 +223,60 @@ def main():
         extra["prefill_1024_at_32768_ms"] = round(ms, 4)
         extra["prefill_tflops"] = round(tflops, 1)
         extra["prefill_mfma_frac"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
+        extra.update(deltanet_extras(ops, torch, args.steps))
         result["extra"] = extra
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(ops, torch, n)
     print(json.dumps(result), flush=True)
+
+
+def deltanet_extras(ops, torch, steps, L=36):
+    """Gated DeltaNet layers (36 of them, each with its own 6.3 MB state): one decode token per layer, a 7-token
+    verify with the lazy commit of the first token (both as HIP-graph replays of the 36 layers, which is how the
+    engine issues its decode step), and a 1024-token prefill chunk.  Algorithmic HBM bytes per decode
+    layer: the state read and written (2 x 48 x 128 x 128 x 4) plus the conv window, weights and token rows."""
+    ch, vd, vh = ops.DN_CH, ops.DN_VD, ops.DN_VH
+    g = torch.Generator(device="cuda").manual_seed(5)
+    rn = lambda *s, sc=1.0: torch.randn(*s, device="cuda", generator=g) * sc
+    layers = [ops.DNParams(rn(ch, 4, sc=0.5), rn(vh), -torch.exp(rn(vh, sc=0.5)), 1.0 + rn(128, sc=0.1),
+                           rn(2, 3, ch, sc=0.5), rn(vh, 128, 128, sc=0.1)) for _ in range(L)]
+    qkv, z = rn(7, ch, sc=0.5), rn(7, vd)
+    b, a = rn(7, 64), rn(7, 64, sc=2.0)
+    o = torch.empty((7, vd), device="cuda")
+    tk1 = ops.DNTokens(qkv=qkv, z=z, beta=b, alpha=a)
+
+    def dec():
+        for p in layers:
+            ops.deltanet_multi(p, 0, tk1, 0, 1, 1, 1e-6, o)
+    out = {}
+    ms = time_graph(torch, dec, max(10, steps))
+    us = ms * 1000.0 / L
+    state_bytes = 2 * vh * 128 * 128 * 4
+    dec_bytes = state_bytes + 6 * ch * 4 + ch * 16 + (ch + 2 * vd) * 4  # + conv window r/w, conv_w, rows
+    out["deltanet_decode_us_per_layer"] = round(us, 3)
+    out["deltanet_decode_gbs"] = round(dec_bytes / (us * 1e-6) / 1e9, 1)
+    sq, sb, sa = torch.empty_like(qkv), torch.empty_like(b), torch.empty_like(a)
+    tk7 = ops.DNTokens(qkv=qkv, z=z, beta=b, alpha=a, oqkv=sq, obeta=sb, oalpha=sa)
+
+    def ver():
+        for p in layers:
+            ops.deltanet_multi(p, 0, tk7, 0, 7, 1, 1e-6, o)
+    ms = time_graph(torch, ver, max(5, steps // 2))
+    out["deltanet_verify7_us_per_layer"] = round(ms * 1000.0 / L, 3)
+    B = 1024
+    xq, xz = rn(B, ch, sc=0.5), rn(B, vd)
+    xb, xa = rn(B, vh), rn(B, vh, sc=2.0)
+    work = torch.empty(ops.dn_work_bytes(B) // 4, device="cuda")
+    core = torch.empty((B, vd), device="cuda")
+    o16 = torch.empty((B, vd), dtype=torch.float16, device="cuda")
+    p0 = layers[0]
+    ms = time_calls(torch, lambda: ops.deltanet_rows(p0, xq, xz, xb, xa, B, 0, 1e-6, work, core, o16), 10, 2)
+    out["deltanet_prefill_1024_ms"] = round(ms, 4)
+    out["deltanet_prefill_tokens_per_s"] = round(B / (ms * 1e-3), 0)
+    del layers
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(ops, torch, n):

@@ -8,11 +8,13 @@
 // entry points and state conventions: src/cuda/ops.cuh:54-97 (decode, lazy commit), src/cuda/prefill.cuh:37-44
 // (prefill rows).
 //
-// Decode / verify (k_dn_multi): one workgroup of 8 waves per value head (48 workgroups).  The head's state stays in
-// registers for the whole call: lane (column 16 w + l / 4, row group l % 4) of wave w holds the 32 rows
-// 32 (l % 4) .. + 31 of its column, so both dot products per column reduce over 4 lanes (two quad-permute adds).
-// Tokens are applied one after the other with the same code, so a token sequence gives the same bits however it is
-// split into calls (the lazy-commit contract, src/cuda/ops.cuh:93-95).
+// Decode / verify (k_dn_head): one workgroup of 16 waves per value head holds the head's 64 KB state in registers
+// (8 lanes per column), loaded and stored with 128 contiguous bytes per column per instruction.  All of a chunk's
+// inputs are loaded up front in one round trip; the conv and the per-token scalars (norms, q.k, beta, decay) are
+// computed before the sequential delta rule, which then runs without barriers; the gated RMSNorm, ActQ8 and the
+// mapped-host copy finish inside the same kernel.  Tokens are applied one after the other with the same code, so a
+// token sequence gives the same bits however it is split into calls (the lazy-commit contract,
+// src/cuda/ops.cuh:93-95).
 //
 // Prefill (B tokens): token-parallel conv, conv-window and q/k-normalisation kernels, the sequential recurrence over
 // (48 heads x 4 groups of 32 columns) with the tokens' q / k / v staged in LDS, and the gated norm to fp16.
@@ -42,170 +44,243 @@ __device__ __forceinline__ float quad_sum(float x) {
 }
 
 // ------------------------------------------------------------------------------------------------------- decode
-__global__ void __launch_bounds__(512) k_dn_multi(qwa_dn_params p, int cin, qwa_dn_tokens in, int n_commit,
-                                                  int n_new, int write_after, float eps, float* __restrict__ o,
-                                                  qwa_act_q8 oq, int do_q) {
+constexpr int DN_TC = 8;  // tokens per chunk
+
+// DPP lane moves within a row of 16 lanes (no LDS round trip)
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// sum over the 16 lanes of a DPP row: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror (lane i <-> 7 - i),
+// row_mirror (lane i <-> 15 - i).  Every lane gets the same bits (each step adds the same two values, swapped).
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_mov<0xB1>(x);
+    x += dpp_mov<0x4E>(x);
+    x += dpp_mov<0x141>(x);
+    return x + dpp_mov<0x140>(x);
+}
+
+// a0 . b0 + a1 . b1 over 8 values, as two interleaved fma chains
+__device__ __forceinline__ float dot8(float4 a0, float4 a1, float4 b0, float4 b1) {
+    float x = a0.x * b0.x, y = a0.y * b0.y;
+    x = fmaf(a0.z, b0.z, x);
+    y = fmaf(a0.w, b0.w, y);
+    x = fmaf(a1.x, b1.x, x);
+    y = fmaf(a1.y, b1.y, y);
+    x = fmaf(a1.z, b1.z, x);
+    y = fmaf(a1.w, b1.w, y);
+    return x + y;
+}
+
+// k_dn_head: one workgroup of 16 waves per value head (48 workgroups), the whole call in one kernel.  Lane
+// (column j = t / 8, r8 = t % 8) holds the row quads r8, r8 + 8, r8 + 16, r8 + 24 of its column; the dot products
+// reduce over 8 lanes.  Per chunk of DN_TC tokens: (1) the chunk's inputs (branch-free addresses, one round trip) and the conv
+// over the 384 channels of the head, beta / decay, the gate inputs z; (2) |q|^2, |k|^2, q.k; (3) the delta rule;
+// (4) the gated RMSNorm of the chunk's new tokens over the head's 128 outputs, ActQ8 and the mapped-host copy.
+constexpr int DN_HT = 1024;          // threads of k_dn_head
+
+// sum over 8 aligned lanes (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror); same bits in every lane
+__device__ __forceinline__ float oct_sum(float x) {
+    x += dpp_mov<0xB1>(x);
+    x += dpp_mov<0x4E>(x);
+    return x + dpp_mov<0x141>(x);
+}
+
+__global__ void __launch_bounds__(DN_HT) k_dn_head(qwa_dn_params p, int cin, qwa_dn_tokens in, int n_commit,
+                                                   int n_new, int write_after, float eps, float* __restrict__ o,
+                                                   qwa_act_q8 oq, int do_q) {
     const int h = blockIdx.x, kh = h % DN_KH, t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63;
-    __shared__ __attribute__((aligned(16))) float s_q[DN_KPAD], s_k[DN_KPAD];
-    __shared__ float s_v[DN_HD], s_o[DN_HD], s_misc[4], s_red[2];
-    __shared__ float s_xc[QWA_DN_MAXN][3 * DN_HD], s_z[QWA_DN_MAXN][DN_HD];
+    __shared__ __attribute__((aligned(16))) float s_q[DN_TC][DN_HD], s_k[DN_TC][DN_HD];
+    __shared__ __attribute__((aligned(16))) float s_sc[DN_TC][8];
+    __shared__ float s_v[DN_TC][DN_HD], s_o[DN_TC][DN_HD], s_beta[DN_TC], s_decay[DN_TC], s_red[DN_TC][2];
     const float* cs_in = p.conv_state + (size_t)cin * 3 * DN_CH;
     float* cs_out = p.conv_state + (size_t)(cin ^ 1) * 3 * DN_CH;
+    constexpr int NCONV = 3 * DN_HD;  // conv threads: q, k of key head kh, v of head h
 
-    // conv channel of this thread: q and k of key head kh, v of value head h
-    int c = 0;
+    // conv channel of threads < 384 (the others hold a valid copy of channel t % 384 and never use it)
+    const int tc = t % NCONV;
+    const int c = tc < DN_HD ? kh * DN_HD + tc : tc < 2 * DN_HD ? DN_QK + kh * DN_HD + (tc - DN_HD)
+                                                              : 2 * DN_QK + h * DN_HD + (tc - 2 * DN_HD);
+    const bool conv_thread = t < NCONV;
+    // the q / k channels are shared by value heads kh, kh + 16, kh + 32: only the first writes them back
+    const bool owner = conv_thread && (tc >= 2 * DN_HD || h < DN_KH);
     float x0 = 0.0f, x1 = 0.0f, x2 = 0.0f;
     float4 w = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (t < 3 * DN_HD) {
-        c = t < DN_HD ? kh * DN_HD + t : t < 2 * DN_HD ? DN_QK + kh * DN_HD + (t - DN_HD) : 2 * DN_QK + h * DN_HD + (t - 2 * DN_HD);
+    if (conv_thread) {
         x0 = cs_in[c];
         x1 = cs_in[DN_CH + c];
         x2 = cs_in[2 * DN_CH + c];
         w = *reinterpret_cast<const float4*>(p.conv_w + (size_t)c * 4);
     }
-    // the q / k channels are shared by value heads kh, kh + 16, kh + 32: only the first writes them back
-    const bool owner = t < 3 * DN_HD && (t >= 2 * DN_HD || h < DN_KH);
-    // the new tokens' conv and gate inputs, read once up front (part of them may live in mapped host memory)
-    if (t < 3 * DN_HD) {
-        for (int ni = 0; ni < n_new; ni++)
-            s_xc[ni][t] = c >= in.qkv_split ? in.qkv_host[(size_t)ni * in.qkv_ld + (c - in.qkv_split)]
-                                            : in.qkv[(size_t)ni * DN_CH + c];
-    } else {
-        const int j = t - 3 * DN_HD, zi = h * DN_HD + j;
-        for (int ni = 0; ni < n_new; ni++)
-            s_z[ni][j] = zi >= in.z_split ? in.z_host[(size_t)ni * in.z_ld + (zi - in.z_split)]
-                                          : in.z[(size_t)ni * DN_VD + zi];
-    }
+    const float dtb = p.dt_bias[h], sa = p.ssm_a[h];
+    const int jn = t & (DN_HD - 1);  // output column of the gated norm
+    const float nw = p.ssm_norm[jn];
 
-    // this lane's 32 state values: column j, rows 32 g .. 32 g + 31 (global layout [h][j][i])
-    const int j = 16 * wave + (lane >> 2), g = lane & 3;
+    // this lane's 16 state values: column j, the row quads r8, r8 + 8, r8 + 16, r8 + 24 (global layout [h][j][i]),
+    // so that each load or store instruction covers 128 contiguous bytes per column
+    const int j = t >> 3, r8 = t & 7;
     float* Sh = p.ssm_state + (size_t)h * DN_HD * DN_HD;
-    float s[32];
+    float4* Sq = reinterpret_cast<float4*>(Sh + (size_t)j * DN_HD) + r8;
+    float s[16];
     {
-        const float4* src = reinterpret_cast<const float4*>(Sh + (size_t)j * DN_HD + 32 * g);
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-            const float4 v = src[r];
+        for (int r = 0; r < 4; r++) {
+            const float4 v = Sq[8 * r];
             s[4 * r] = v.x; s[4 * r + 1] = v.y; s[4 * r + 2] = v.z; s[4 * r + 3] = v.w;
         }
     }
     const float oscale = 1.0f / sqrtf((float)DN_HD);
-    __syncthreads();
-
     const int ntot = n_commit + n_new;
-    for (int i = 0; i < ntot; i++) {
-        const bool is_new = i >= n_commit;
-        const int ni = i - n_commit;
-        const float* beta_raw = is_new ? in.beta + ni * DN_BA_LD : in.sbeta + i * DN_BA_LD;
-        const float* alpha_raw = is_new ? in.alpha + ni * DN_BA_LD : in.salpha + i * DN_BA_LD;
-        // 1) causal conv + SiLU (pending tokens replay their saved inputs)
-        if (t < 3 * DN_HD) {
-            const float xc = is_new ? s_xc[ni][t] : in.sqkv[(size_t)i * DN_CH + c];
-            const float val = dn_silu(w.x * x0 + w.y * x1 + w.z * x2 + w.w * xc);
-            if (t < DN_HD) s_q[dn_pad(t)] = val;
-            else if (t < 2 * DN_HD) s_k[dn_pad(t - DN_HD)] = val;
-            else s_v[t - 2 * DN_HD] = val;
-            x0 = x1;
-            x1 = x2;
-            x2 = xc;
-            if (owner) {
-                if (is_new && in.oqkv) in.oqkv[(size_t)ni * DN_CH + c] = xc;
-                if (i == write_after - 1) {  // the window at the commit point, to the other buffer
-                    cs_out[c] = x0;
-                    cs_out[DN_CH + c] = x1;
-                    cs_out[2 * DN_CH + c] = x2;
-                }
+
+    for (int t0 = 0; t0 < ntot; t0 += DN_TC) {
+        const int nt = min(DN_TC, ntot - t0);
+        // 1) inputs.  Conv threads: the chunk's qkv channel values (pending tokens from the save buffer, new ones
+        //    from qkv or, for channels >= qkv_split, mapped host memory), addresses selected rather than branched on
+        //    so that all loads are in flight together.  Every thread: z of (token t / 128, column t % 128).
+        float zv;
+        {
+            const int tt = t >> 7, i = t0 + tt, ni = i - n_commit, zi = h * DN_HD + jn;
+            const bool use = tt < nt && i >= n_commit;
+            const float* pz = zi >= in.z_split ? in.z_host + (size_t)ni * in.z_ld + (zi - in.z_split)
+                                               : in.z + (size_t)ni * DN_VD + zi;
+            zv = *(use ? pz : p.ssm_norm + jn);
+        }
+        if (conv_thread) {
+            float xa[DN_TC];
+#pragma unroll
+            for (int tt = 0; tt < DN_TC; tt++) {
+                const int i = t0 + tt, ni = i - n_commit;
+                const float* pa = i < n_commit ? in.sqkv + (size_t)i * DN_CH + c
+                                  : c >= in.qkv_split ? in.qkv_host + (size_t)ni * in.qkv_ld + (c - in.qkv_split)
+                                                      : in.qkv + (size_t)ni * DN_CH + c;
+                xa[tt] = *(tt < nt ? pa : cs_in + c);
             }
-        }
-        if (is_new && in.obeta && t == 0) {
-            in.obeta[ni * DN_BA_LD + h] = beta_raw[h];
-            in.oalpha[ni * DN_BA_LD + h] = alpha_raw[h];
-        }
-        __syncthreads();
-        // 2) L2 norms of q (wave 0) and k (wave 1); beta and decay (wave 2)
-        if (wave < 2) {
-            const float* src = wave == 0 ? s_q : s_k;
-            const float a0 = src[dn_pad(lane)], a1 = src[dn_pad(lane + 64)];
-            const float sum = wave_sum(a0 * a0 + a1 * a1);
-            if (lane == 0) s_misc[wave] = 1.0f / fmaxf(sqrtf(sum), eps);
-        } else if (wave == 2 && lane == 0) {
-            const float a = alpha_raw[h] + p.dt_bias[h];
-            const float sp = a > 20.0f ? a : logf(1.0f + expf(a));
-            s_misc[2] = 1.0f / (1.0f + expf(-beta_raw[h]));
-            s_misc[3] = expf(sp * p.ssm_a[h]);
-        }
-        __syncthreads();
-        // 3) the gated delta rule on this lane's 32 state values
-        const float qs = s_misc[0], ks = s_misc[1], beta = s_misc[2], decay = s_misc[3];
-        float kr[32], qr[32];
+            // causal conv + SiLU, the window sliding per thread; saves and the window at the commit point
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-            const float4 k4 = *reinterpret_cast<const float4*>(&s_k[36 * g + 4 * r]);
-            const float4 q4 = *reinterpret_cast<const float4*>(&s_q[36 * g + 4 * r]);
-            kr[4 * r] = k4.x * ks; kr[4 * r + 1] = k4.y * ks; kr[4 * r + 2] = k4.z * ks; kr[4 * r + 3] = k4.w * ks;
-            qr[4 * r] = q4.x * qs; qr[4 * r + 1] = q4.y * qs; qr[4 * r + 2] = q4.z * qs; qr[4 * r + 3] = q4.w * qs;
-        }
-        float ka = 0.0f, kb = 0.0f, kc = 0.0f, kd = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 8; r++) {
-            s[4 * r] *= decay; s[4 * r + 1] *= decay; s[4 * r + 2] *= decay; s[4 * r + 3] *= decay;
-            ka = fmaf(s[4 * r], kr[4 * r], ka);
-            kb = fmaf(s[4 * r + 1], kr[4 * r + 1], kb);
-            kc = fmaf(s[4 * r + 2], kr[4 * r + 2], kc);
-            kd = fmaf(s[4 * r + 3], kr[4 * r + 3], kd);
-        }
-        const float kv = quad_sum((ka + kb) + (kc + kd));  // (S^T k)_j over the column's 128 rows
-        const float delta = (s_v[j] - kv) * beta;
-        float oa = 0.0f, ob = 0.0f, oc = 0.0f, od = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 8; r++) {
-            s[4 * r] = fmaf(kr[4 * r], delta, s[4 * r]);
-            s[4 * r + 1] = fmaf(kr[4 * r + 1], delta, s[4 * r + 1]);
-            s[4 * r + 2] = fmaf(kr[4 * r + 2], delta, s[4 * r + 2]);
-            s[4 * r + 3] = fmaf(kr[4 * r + 3], delta, s[4 * r + 3]);
-            oa = fmaf(s[4 * r], qr[4 * r], oa);
-            ob = fmaf(s[4 * r + 1], qr[4 * r + 1], ob);
-            oc = fmaf(s[4 * r + 2], qr[4 * r + 2], oc);
-            od = fmaf(s[4 * r + 3], qr[4 * r + 3], od);
-        }
-        const float oj = quad_sum((oa + ob) + (oc + od));
-        if (is_new && g == 0) s_o[j] = oj * oscale;
-        if (i == write_after - 1) {  // the state at the commit point, in place
-            float4* dst = reinterpret_cast<float4*>(Sh + (size_t)j * DN_HD + 32 * g);
-#pragma unroll
-            for (int r = 0; r < 8; r++) dst[r] = make_float4(s[4 * r], s[4 * r + 1], s[4 * r + 2], s[4 * r + 3]);
-        }
-        // 4) new tokens: gated RMSNorm rmsnorm(o) * ssm_norm * silu(z), optional ActQ8 and mapped-host copy
-        if (is_new) {
-            __syncthreads();
-            if (wave < 2) {
-                const float v = s_o[t];
-                const float sum = wave_sum(v * v);
-                if (lane == 0) s_red[wave] = sum;
-            }
-            __syncthreads();
-            if (wave < 2) {
-                const float rs = 1.0f / sqrtf((s_red[0] + s_red[1]) / DN_HD + eps);
-                const float v = s_o[t] * rs * p.ssm_norm[t] * dn_silu(s_z[ni][t]);
-                const size_t oi = (size_t)ni * DN_VD + h * DN_HD + t;
-                o[oi] = v;
-                if (in.o_host) in.o_host[oi] = v;
-                if (do_q) {
-                    // ActQ8 (src/cuda/common.cuh:188-197) per 32 outputs: d = amax / 127, q = rint(v / d), s = d sum(q)
-                    const float amax = half_max(fabsf(v));
-                    const float db = amax / 127.0f;
-                    const int qi = db > 0.0f ? (int)__builtin_rintf(v / db) : 0;
-                    oq.q[oi] = (int8_t)qi;
-                    const float qsum = half_sum((float)qi);
-                    if ((lane & 31) == 0) {
-                        const size_t blk = (size_t)ni * (DN_VD / 32) + h * 4 + (t >> 5);
-                        oq.d[blk] = db;
-                        oq.s[blk] = db * qsum;
+            for (int tt = 0; tt < DN_TC; tt++) {
+                if (tt < nt) {
+                    const int i = t0 + tt;
+                    const float val = dn_silu(fmaf(w.w, xa[tt], fmaf(w.z, x2, fmaf(w.y, x1, w.x * x0))));
+                    x0 = x1; x1 = x2; x2 = xa[tt];
+                    if (tc < DN_HD) s_q[tt][tc] = val;
+                    else if (tc < 2 * DN_HD) s_k[tt][tc - DN_HD] = val;
+                    else s_v[tt][tc - 2 * DN_HD] = val;
+                    if (owner) {
+                        if (i >= n_commit && in.oqkv) in.oqkv[(size_t)(i - n_commit) * DN_CH + c] = xa[tt];
+                        if (i == write_after - 1) {
+                            cs_out[c] = x0;
+                            cs_out[DN_CH + c] = x1;
+                            cs_out[2 * DN_CH + c] = x2;
+                        }
                     }
                 }
             }
+        } else if (wave == DN_HT / 64 - 1 && lane < nt) {  // beta and decay of token t0 + lane
+            const int i = t0 + lane;
+            const bool is_new = i >= n_commit;
+            const float* brow = is_new ? in.beta + (i - n_commit) * DN_BA_LD : in.sbeta + i * DN_BA_LD;
+            const float* arow = is_new ? in.alpha + (i - n_commit) * DN_BA_LD : in.salpha + i * DN_BA_LD;
+            const float br = brow[h], ar = arow[h];
+            const float x = ar + dtb;
+            const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
+            s_beta[lane] = 1.0f / (1.0f + expf(-br));
+            s_decay[lane] = expf(sp * sa);
+            if (is_new && in.obeta) {
+                in.obeta[(i - n_commit) * DN_BA_LD + h] = br;
+                in.oalpha[(i - n_commit) * DN_BA_LD + h] = ar;
+            }
         }
+        __syncthreads();
+        // 2) per token: |q|^2, |k|^2 and q.k (16 lanes, 8 elements each), folded into the scalars of step 3
+        if (t < 16 * DN_TC) {
+            const int tt = t >> 4, r16 = t & 15;
+            if (tt < nt) {
+                const int e = 8 * r16;
+                const float4 q0 = *reinterpret_cast<const float4*>(&s_q[tt][e]);
+                const float4 q1 = *reinterpret_cast<const float4*>(&s_q[tt][e + 4]);
+                const float4 k0 = *reinterpret_cast<const float4*>(&s_k[tt][e]);
+                const float4 k1 = *reinterpret_cast<const float4*>(&s_k[tt][e + 4]);
+                const float qq = row16_sum(dot8(q0, q1, q0, q1));
+                const float kk = row16_sum(dot8(k0, k1, k0, k1));
+                const float kq = row16_sum(dot8(k0, k1, q0, q1));
+                if (r16 == 0) {
+                    const float qs = 1.0f / fmaxf(sqrtf(qq), eps), ks = 1.0f / fmaxf(sqrtf(kk), eps);
+                    const float decay = s_decay[tt], beta = s_beta[tt];
+                    *reinterpret_cast<float4*>(&s_sc[tt][0]) =
+                        make_float4(decay, decay * ks, beta * ks, qs * oscale * decay);
+                    s_sc[tt][4] = qs * oscale * kq;
+                }
+            }
+        }
+        __syncthreads();
+        // 3) the gated delta rule, token after token, on this lane's 16 state values, in the form
+        //      sk = S^T k_raw, sq = S^T q_raw (old state; both reductions run interleaved)
+        //      dk = (v - decay ks sk) beta ks,  o = qs / sqrt(128) (decay sq + (q.k) dk),  S = decay S + k_raw dk
+        //    which equals S <- decay S; S += k ((v - S^T k) beta)^T; o = S^T q / sqrt(128) with unit q, k.
+        for (int tt = 0; tt < nt; tt++) {
+            const float4* kp = reinterpret_cast<const float4*>(&s_k[tt][0]) + r8;  // quad r8 + 8 r at kp[8 r]
+            const float4* qp = reinterpret_cast<const float4*>(&s_q[tt][0]) + r8;
+            const float4 cc = *reinterpret_cast<const float4*>(&s_sc[tt][0]);
+            const float c2 = s_sc[tt][4], v = s_v[tt][j];
+            float ka = 0.0f, kb = 0.0f, qa = 0.0f, qb = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float4 k4 = kp[8 * r], q4 = qp[8 * r];
+                ka = fmaf(s[4 * r], k4.x, ka);
+                kb = fmaf(s[4 * r + 1], k4.y, kb);
+                qa = fmaf(s[4 * r], q4.x, qa);
+                qb = fmaf(s[4 * r + 1], q4.y, qb);
+                ka = fmaf(s[4 * r + 2], k4.z, ka);
+                kb = fmaf(s[4 * r + 3], k4.w, kb);
+                qa = fmaf(s[4 * r + 2], q4.z, qa);
+                qb = fmaf(s[4 * r + 3], q4.w, qb);
+            }
+            const float sk = oct_sum(ka + kb), sq = oct_sum(qa + qb);
+            const float dk = fmaf(-cc.y, sk, v) * cc.z;
+            const float oj = fmaf(cc.w, sq, c2 * dk);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {  // k read again from LDS rather than held in 16 more registers
+                const float4 k4 = kp[8 * r];
+                s[4 * r] = fmaf(k4.x, dk, s[4 * r] * cc.x);
+                s[4 * r + 1] = fmaf(k4.y, dk, s[4 * r + 1] * cc.x);
+                s[4 * r + 2] = fmaf(k4.z, dk, s[4 * r + 2] * cc.x);
+                s[4 * r + 3] = fmaf(k4.w, dk, s[4 * r + 3] * cc.x);
+            }
+            if (r8 == 0) s_o[tt][j] = oj;
+            if (t0 + tt == write_after - 1) {  // the state at the commit point, in place
+#pragma unroll
+                for (int r = 0; r < 4; r++) Sq[8 * r] = make_float4(s[4 * r], s[4 * r + 1], s[4 * r + 2], s[4 * r + 3]);
+            }
+        }
+        __syncthreads();
+        // 4) gated RMSNorm of the chunk's new tokens: thread (token t / 128, column t % 128)
+        const int tt = t >> 7, i = t0 + tt;
+        const bool emit = tt < nt && i >= n_commit;
+        const float y0 = s_o[tt][jn];
+        const float ss = wave_sum(y0 * y0);
+        if (lane == 0) s_red[tt][wave & 1] = ss;
+        __syncthreads();
+        if (emit) {
+            const float rs = 1.0f / sqrtf((s_red[tt][0] + s_red[tt][1]) / DN_HD + eps);
+            const float y = y0 * rs * nw * dn_silu(zv);
+            const size_t oi = (size_t)(i - n_commit) * DN_VD + h * DN_HD + jn;
+            o[oi] = y;
+            if (in.o_host) in.o_host[oi] = y;
+            if (do_q) {
+                // ActQ8 (src/cuda/common.cuh:188-197) per 32 outputs: d = amax / 127, q = rint(y / d), s = d sum(q)
+                const float amax = half_max(fabsf(y));
+                const float db = amax / 127.0f;
+                const int qi = db > 0.0f ? (int)__builtin_rintf(y / db) : 0;
+                oq.q[oi] = (int8_t)qi;
+                const float qsum = half_sum((float)qi);
+                if ((lane & 31) == 0) {
+                    oq.d[oi / 32] = db;
+                    oq.s[oi / 32] = db * qsum;
+                }
+            }
+        }
+        // the next chunk rewrites s_q .. s_o only after every thread has passed this point
         __syncthreads();
     }
     if (in.o_host) __threadfence_system();
@@ -392,7 +467,7 @@ __global__ void __launch_bounds__(128) k_dn_gnorm_rows(const float* __restrict__
 hipError_t launch_dn_multi(const qwa_dn_params& p, int cin, const qwa_dn_tokens& in, int n_commit, int n_new,
                            int write_after, float eps, float* o, const qwa_act_q8* oq, hipStream_t st) {
     const qwa_act_q8 a = oq ? *oq : qwa_act_q8{nullptr, nullptr, nullptr};
-    hipLaunchKernelGGL(k_dn_multi, dim3(DN_VH), dim3(512), 0, st, p, cin, in, n_commit, n_new, write_after, eps, o,
+    hipLaunchKernelGGL(k_dn_head, dim3(DN_VH), dim3(DN_HT), 0, st, p, cin, in, n_commit, n_new, write_after, eps, o,
                        a, oq != nullptr ? 1 : 0);
     return hipGetLastError();
 }

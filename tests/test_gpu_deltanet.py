@@ -243,3 +243,24 @@ def test_rows_then_decode_continues(gpu, oracle):
         assert rel_l2(out[t], o_ref[40 + t]) < RTOL, t
     assert rel_l2(gpu_state(p), S_ref) < RTOL
     assert np.array_equal(p.conv_state[0].cpu().numpy(), cs_ref)
+
+
+def test_multi_many_pending_matches_steps_bitwise(gpu):
+    """6 pending + 7 new tokens in one call (more than one internal chunk of tokens) and a commit point inside the
+    new tokens: outputs, state and conv window equal one step per token up to that point."""
+    L = Layer(15, 0.1, 0.5)
+    qkv, z, b, a = L.tokens(13)
+    pa = L.device(0)
+    steps(pa, qkv[:10], z[:10], b[:10], a[:10])  # the state and window after 10 tokens
+    ref_after_all = L.device(0)
+    out_all, _ = steps(ref_after_all, qkv, z, b, a)
+    pb = L.device(0)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    o = torch.empty((7, VD), device="cuda")
+    tk = ops.DNTokens(sqkv=dev(qkv[:6]), sbeta=dev(b[:6]), salpha=dev(a[:6]), qkv=dev(qkv[6:]), z=dev(z[6:]),
+                      beta=dev(b[6:]), alpha=dev(a[6:]))
+    ops.deltanet_multi(pb, 0, tk, 6, 7, 10, EPS, o)
+    torch.cuda.synchronize()
+    assert np.array_equal(o.cpu().numpy().view(np.uint32), out_all[6:].view(np.uint32))
+    assert torch.equal(pb.ssm_state, pa.ssm_state)
+    assert torch.equal(pb.conv_state[1], pa.conv_state[0])  # 10 steps from buffer 0 end in buffer 0
