@@ -17,7 +17,7 @@
 // src/cuda/ops.cuh:93-95).
 //
 // Prefill (B tokens): token-parallel conv, conv-window and q/k-normalisation kernels, the sequential recurrence over
-// (48 heads x 4 groups of 32 columns) with the tokens' q / k / v staged in LDS, and the gated norm to fp16.
+// (48 heads x 8 groups of 16 columns) with the tokens' q / k / v staged in LDS, and the gated norm to fp16.
 #include <type_traits>
 
 #include "launch.hpp"
@@ -32,17 +32,8 @@ constexpr int DN_KH = 16;
 constexpr int DN_VH = 48;
 constexpr int DN_VD = DN_VH * DN_HD;  // 6144
 constexpr int DN_BA_LD = 64;          // row stride of the decode path's beta / alpha inputs
-constexpr int DN_KPAD = DN_HD + 16;   // padded q / k row in LDS: element i at i + 4 (i / 32)
 
 __device__ __forceinline__ float dn_silu(float x) { return x / (1.0f + __expf(-x)); }
-__device__ __forceinline__ int dn_pad(int i) { return i + 4 * (i >> 5); }
-
-// sum over the 4 lanes of a quad (the 4 row groups of one state column)
-__device__ __forceinline__ float quad_sum(float x) {
-    x += __shfl_xor(x, 1, 64);
-    return x + __shfl_xor(x, 2, 64);
-}
-
 // ------------------------------------------------------------------------------------------------------- decode
 constexpr int DN_TC = 8;  // tokens per chunk
 
@@ -293,6 +284,7 @@ struct DnRows {
     float* kn;     // [B][2048] L2-normalised k
     float* beta;   // [B][48]
     float* decay;  // [B][48]
+    float* kq;     // [B][16] qn . kn per key head
 };
 
 __host__ __device__ inline DnRows dn_rows_split(void* work, int B) {
@@ -307,10 +299,12 @@ __host__ __device__ inline DnRows dn_rows_split(void* work, int B) {
     r.beta = f;
     f += (size_t)B * DN_VH;
     r.decay = f;
+    f += (size_t)B * DN_VH;
+    r.kq = f;
     return r;
 }
 
-size_t dn_work_bytes(int B) { return (size_t)B * (DN_CH + 2 * DN_QK + 2 * DN_VH) * sizeof(float); }
+size_t dn_work_bytes(int B) { return (size_t)B * (DN_CH + 2 * DN_QK + 2 * DN_VH + DN_KH) * sizeof(float); }
 
 // out[t][c] = silu(sum_k w[c][k] in(t - 3 + k)), in(i) = qkv[i][c] for i >= 0, else row 3 + i of the old window
 __global__ void __launch_bounds__(256) k_dn_conv_rows(const float* __restrict__ qkv, const float* __restrict__ cs_old,
@@ -339,21 +333,28 @@ __global__ void __launch_bounds__(256) k_dn_conv_state(const float* __restrict__
     }
 }
 
-// per token: L2-normalised q and k of the 16 key heads (wave w: heads w, w + 4, ... of q then k), beta and decay
+// per token: L2-normalised q and k of the 16 key heads and their dot product (wave w: key heads w, w + 4, ...),
+// beta and decay
 __global__ void __launch_bounds__(256) k_dn_prep_rows(DnRows r, const float* __restrict__ beta_raw,
                                                       const float* __restrict__ alpha_raw,
                                                       const float* __restrict__ dt_bias,
                                                       const float* __restrict__ ssm_a, float eps) {
     const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int jn = wave; jn < 2 * DN_KH; jn += 4) {
-        const bool is_k = jn >= DN_KH;
-        const int kh = jn % DN_KH;
-        const float* src = r.conv + (size_t)t * DN_CH + (is_k ? DN_QK : 0) + kh * DN_HD;
-        const float a0 = src[lane], a1 = src[lane + 64];
-        const float inv = 1.0f / fmaxf(sqrtf(wave_sum(a0 * a0 + a1 * a1)), eps);
-        float* dst = (is_k ? r.kn : r.qn) + (size_t)t * DN_QK + kh * DN_HD;
-        dst[lane] = a0 * inv;
-        dst[lane + 64] = a1 * inv;
+    for (int kh = wave; kh < DN_KH; kh += 4) {
+        const float* qs = r.conv + (size_t)t * DN_CH + kh * DN_HD;
+        const float* ks = qs + DN_QK;
+        const float q0 = qs[lane], q1 = qs[lane + 64], k0 = ks[lane], k1 = ks[lane + 64];
+        const float iq = 1.0f / fmaxf(sqrtf(wave_sum(q0 * q0 + q1 * q1)), eps);
+        const float ik = 1.0f / fmaxf(sqrtf(wave_sum(k0 * k0 + k1 * k1)), eps);
+        const float qa = q0 * iq, qb = q1 * iq, ka = k0 * ik, kb = k1 * ik;
+        float* qd = r.qn + (size_t)t * DN_QK + kh * DN_HD;
+        float* kd = r.kn + (size_t)t * DN_QK + kh * DN_HD;
+        qd[lane] = qa;
+        qd[lane + 64] = qb;
+        kd[lane] = ka;
+        kd[lane + 64] = kb;
+        const float kq = wave_sum(qa * ka + qb * kb);
+        if (lane == 0) r.kq[(size_t)t * DN_KH + kh] = kq;
     }
     if (threadIdx.x < DN_VH) {
         const int h = threadIdx.x;
@@ -364,88 +365,111 @@ __global__ void __launch_bounds__(256) k_dn_prep_rows(DnRows r, const float* __r
     }
 }
 
-// The recurrence over B tokens: grid (48 heads, 4 groups of 32 columns), 2 waves; lane (column 16 w + l / 4 of the
-// group, row group l % 4) holds 32 rows of its column for the whole call.  DN_RT tokens at a time are staged in LDS
-// (q / k rows padded so that the 4 row groups read different banks).  core_out may alias qkv: it is written only
-// after the conv kernel has read qkv.
-constexpr int DN_RT = 16;
-constexpr int DN_RCOL = 32;
-__global__ void __launch_bounds__(128) k_dn_recur_rows(DnRows r, float* __restrict__ state, int B,
+// The recurrence over B tokens: grid (48 heads, 8 groups of 16 columns), 4 waves.  Lane (column jc = t / 16 of the
+// group, r16 = t % 16) holds the row quads r16 and r16 + 16 of its column for the whole call (each load / store
+// instruction covers 256 contiguous bytes per column).  Per token, with unit q, k and kq = q.k:
+//     sk = S^T k, sq = S^T q;  dk = (v - decay sk) beta;  o = decay sq + kq dk;  S = decay S + k dk^T
+// (the reference's S <- decay S; S += k ((v - S^T k) beta)^T; o = S^T q).  Blocks of DN_RT tokens are staged in LDS
+// double buffers; the next block's global loads are in flight while the current block computes.  core_out may alias
+// qkv: it is written only after the conv kernel has read qkv.
+constexpr int DN_RT = 16;                 // tokens per staged block
+constexpr int DN_RG = 8;                  // workgroups (column groups) per head
+constexpr int DN_RC = DN_HD / DN_RG;      // 16 columns per workgroup
+__global__ void __launch_bounds__(256) k_dn_recur_rows(DnRows r, float* __restrict__ state, int B,
                                                        float* __restrict__ core_out) {
-    const int h = blockIdx.x, cgp = blockIdx.y, kh = h % DN_KH;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane & 3;
-    const int jc = 16 * wave + (lane >> 2), col = cgp * DN_RCOL + jc;
-    __shared__ __attribute__((aligned(16))) float sk[DN_RT][DN_KPAD], sq[DN_RT][DN_KPAD];
-    __shared__ float sv[DN_RT][DN_RCOL], so[DN_RT][DN_RCOL], sbeta[DN_RT], sdecay[DN_RT];
-    float* Sh = state + (size_t)h * DN_HD * DN_HD;
-    float s[32];
-    {
-        const float4* src = reinterpret_cast<const float4*>(Sh + (size_t)col * DN_HD + 32 * g);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 v = src[i];
-            s[4 * i] = v.x; s[4 * i + 1] = v.y; s[4 * i + 2] = v.z; s[4 * i + 3] = v.w;
-        }
-    }
+    const int h = blockIdx.x, grp = blockIdx.y, kh = h % DN_KH, t = threadIdx.x;
+    const int jc = t >> 4, r16 = t & 15, j = grp * DN_RC + jc;
+    __shared__ float4 sk[2][DN_RT][DN_HD / 4], sq[2][DN_RT][DN_HD / 4];
+    __shared__ float4 sc[2][DN_RT];  // decay, beta, kq
+    __shared__ float sv[2][DN_RT][DN_RC], so[DN_RT][DN_RC];
+    float4* Sq = reinterpret_cast<float4*>(state + (size_t)h * DN_HD * DN_HD + (size_t)j * DN_HD) + r16;
+    const float4 s0 = Sq[0], s1 = Sq[16];
+    float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     const float oscale = 1.0f / sqrtf((float)DN_HD);
-    for (int t0 = 0; t0 < B; t0 += DN_RT) {
-        const int nt = min(DN_RT, B - t0);
-        __syncthreads();  // the previous group's outputs are written out
-        for (int i = threadIdx.x; i < nt * DN_HD; i += 128) {
-            const int tt = i / DN_HD, e = i % DN_HD;
-            sk[tt][dn_pad(e)] = r.kn[(size_t)(t0 + tt) * DN_QK + kh * DN_HD + e];
-            sq[tt][dn_pad(e)] = r.qn[(size_t)(t0 + tt) * DN_QK + kh * DN_HD + e];
-        }
-        for (int i = threadIdx.x; i < nt * DN_RCOL; i += 128) {
-            const int tt = i / DN_RCOL, e = i % DN_RCOL;
-            sv[tt][e] = r.conv[(size_t)(t0 + tt) * DN_CH + 2 * DN_QK + h * DN_HD + cgp * DN_RCOL + e];
-        }
-        if (threadIdx.x < nt) {
-            sbeta[threadIdx.x] = r.beta[(size_t)(t0 + threadIdx.x) * DN_VH + h];
-            sdecay[threadIdx.x] = r.decay[(size_t)(t0 + threadIdx.x) * DN_VH + h];
-        }
-        __syncthreads();
-        for (int tt = 0; tt < nt; tt++) {
-            const float4* kp = reinterpret_cast<const float4*>(&sk[tt][36 * g]);
-            const float4* qp = reinterpret_cast<const float4*>(&sq[tt][36 * g]);
-            const float decay = sdecay[tt], beta = sbeta[tt];
-            float ka = 0.0f, kb = 0.0f, kc = 0.0f, kd = 0.0f;
+
+    // staging: thread (token tt = t / 16, f = t % 16) moves float4 f and f + 16 of q and k, v column f, and (t < 16)
+    // the scalars of token t; slots past B read token 0 and are not used
+    const int st_tt = t >> 4, st_f = t & 15;
+    float4 pk0, pk1, pq0, pq1, pc;
+    float pv;
+    auto fetch = [&](int b0) {
+        const int i = min(b0 + st_tt, B - 1);
+        const float4* kr = reinterpret_cast<const float4*>(r.kn + (size_t)i * DN_QK + kh * DN_HD);
+        const float4* qr = reinterpret_cast<const float4*>(r.qn + (size_t)i * DN_QK + kh * DN_HD);
+        pk0 = kr[st_f];
+        pk1 = kr[st_f + 16];
+        pq0 = qr[st_f];
+        pq1 = qr[st_f + 16];
+        pv = r.conv[(size_t)i * DN_CH + 2 * DN_QK + h * DN_HD + grp * DN_RC + st_f];
+        const int ic = min(b0 + t, B - 1);
+        if (t < DN_RT)
+            pc = make_float4(r.decay[(size_t)ic * DN_VH + h], r.beta[(size_t)ic * DN_VH + h],
+                             r.kq[(size_t)ic * DN_KH + kh], 0.0f);
+    };
+    auto stage = [&](int buf) {
+        sk[buf][st_tt][st_f] = pk0;
+        sk[buf][st_tt][st_f + 16] = pk1;
+        sq[buf][st_tt][st_f] = pq0;
+        sq[buf][st_tt][st_f + 16] = pq1;
+        sv[buf][st_tt][st_f] = pv;
+        if (t < DN_RT) sc[buf][t] = pc;
+    };
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int b0 = 0, buf = 0; b0 < B; b0 += DN_RT, buf ^= 1) {
+        const int nt = min(DN_RT, B - b0);
+        if (b0 + DN_RT < B) fetch(b0 + DN_RT);
+        // two operand sets alternate so that the next token's LDS reads overlap the current token's arithmetic
+        struct Op {
+            float4 ka, kb, qa, qb, c;
+            float v;
+        };
+        auto load = [&](Op& op, int tt) {
+            op.ka = sk[buf][tt][r16];
+            op.kb = sk[buf][tt][r16 + 16];
+            op.qa = sq[buf][tt][r16];
+            op.qb = sq[buf][tt][r16 + 16];
+            op.c = sc[buf][tt];
+            op.v = sv[buf][tt][jc];
+        };
+        auto apply = [&](const Op& op, int tt) {
+            const float kr[8] = {op.ka.x, op.ka.y, op.ka.z, op.ka.w, op.kb.x, op.kb.y, op.kb.z, op.kb.w};
+            const float qr[8] = {op.qa.x, op.qa.y, op.qa.z, op.qa.w, op.qb.x, op.qb.y, op.qb.z, op.qb.w};
+            float k0 = 0.0f, k1 = 0.0f, q0 = 0.0f, q1 = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 k4 = kp[i];
-                s[4 * i] *= decay; s[4 * i + 1] *= decay; s[4 * i + 2] *= decay; s[4 * i + 3] *= decay;
-                ka = fmaf(s[4 * i], k4.x, ka);
-                kb = fmaf(s[4 * i + 1], k4.y, kb);
-                kc = fmaf(s[4 * i + 2], k4.z, kc);
-                kd = fmaf(s[4 * i + 3], k4.w, kd);
+            for (int e = 0; e < 4; e++) {
+                k0 = fmaf(s[2 * e], kr[2 * e], k0);
+                k1 = fmaf(s[2 * e + 1], kr[2 * e + 1], k1);
+                q0 = fmaf(s[2 * e], qr[2 * e], q0);
+                q1 = fmaf(s[2 * e + 1], qr[2 * e + 1], q1);
             }
-            const float kv = quad_sum((ka + kb) + (kc + kd));
-            const float delta = (sv[tt][jc] - kv) * beta;
-            float oa = 0.0f, ob = 0.0f, oc = 0.0f, od = 0.0f;
+            const float skv = row16_sum(k0 + k1), sqv = row16_sum(q0 + q1);
+            const float dk = fmaf(-op.c.x, skv, op.v) * op.c.y;
+            const float oj = fmaf(op.c.x, sqv, op.c.z * dk);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 k4 = kp[i], q4 = qp[i];
-                s[4 * i] = fmaf(k4.x, delta, s[4 * i]);
-                s[4 * i + 1] = fmaf(k4.y, delta, s[4 * i + 1]);
-                s[4 * i + 2] = fmaf(k4.z, delta, s[4 * i + 2]);
-                s[4 * i + 3] = fmaf(k4.w, delta, s[4 * i + 3]);
-                oa = fmaf(s[4 * i], q4.x, oa);
-                ob = fmaf(s[4 * i + 1], q4.y, ob);
-                oc = fmaf(s[4 * i + 2], q4.z, oc);
-                od = fmaf(s[4 * i + 3], q4.w, od);
-            }
-            const float ov = quad_sum((oa + ob) + (oc + od));
-            if (g == 0) so[tt][jc] = ov * oscale;
+            for (int e = 0; e < 8; e++) s[e] = fmaf(kr[e], dk, s[e] * op.c.x);
+            if (r16 == 0) so[tt][jc] = oj * oscale;
+        };
+        Op opa, opb;
+        load(opa, 0);
+        for (int tt = 0; tt < nt; tt += 2) {
+            if (tt + 1 < nt) load(opb, tt + 1);
+            apply(opa, tt);
+            if (tt + 1 >= nt) break;
+            if (tt + 2 < nt) load(opa, tt + 2);
+            apply(opb, tt + 1);
         }
+        __syncthreads();  // outputs complete; every read of buffer buf done
+        {
+            const int tt = t >> 4, e = t & 15;
+            if (tt < nt) core_out[(size_t)(b0 + tt) * DN_VD + h * DN_HD + grp * DN_RC + e] = so[tt][e];
+        }
+        if (b0 + DN_RT < B) stage(buf ^ 1);
         __syncthreads();
-        for (int i = threadIdx.x; i < nt * DN_RCOL; i += 128) {
-            const int tt = i / DN_RCOL, e = i % DN_RCOL;
-            core_out[(size_t)(t0 + tt) * DN_VD + h * DN_HD + cgp * DN_RCOL + e] = so[tt][e];
-        }
     }
-    float4* dst = reinterpret_cast<float4*>(Sh + (size_t)col * DN_HD + 32 * g);
-#pragma unroll
-    for (int i = 0; i < 8; i++) dst[i] = make_float4(s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]);
+    Sq[0] = make_float4(s[0], s[1], s[2], s[3]);
+    Sq[16] = make_float4(s[4], s[5], s[6], s[7]);
 }
 
 // gated RMSNorm per (token, value head), fp16 out: grid (B, 48), 128 threads
@@ -481,7 +505,7 @@ hipError_t launch_dn_rows(const qwa_dn_params& p, const float* qkv, const float*
     hipLaunchKernelGGL(k_dn_conv_rows, dim3(DN_CH / 256, B), dim3(256), 0, st, qkv, cs_old, p.conv_w, r.conv);
     hipLaunchKernelGGL(k_dn_conv_state, dim3(DN_CH / 256), dim3(256), 0, st, qkv, cs_old, B, cs_new);
     hipLaunchKernelGGL(k_dn_prep_rows, dim3(B), dim3(256), 0, st, r, beta_raw, alpha_raw, p.dt_bias, p.ssm_a, eps);
-    hipLaunchKernelGGL(k_dn_recur_rows, dim3(DN_VH, DN_HD / DN_RCOL), dim3(128), 0, st, r, p.ssm_state, B, core_out);
+    hipLaunchKernelGGL(k_dn_recur_rows, dim3(DN_VH, DN_RG), dim3(256), 0, st, r, p.ssm_state, B, core_out);
     hipLaunchKernelGGL(k_dn_gnorm_rows, dim3(B, DN_VH), dim3(128), 0, st, core_out, z, p.ssm_norm, eps, o16);
     return hipGetLastError();
 }
