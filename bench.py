@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--positions", type=int, default=150000)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="headline decode only")
+    ap.add_argument("--deltanet-only", action="store_true",
+                    help="print only the Gated DeltaNet figures (for profiling those kernels)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run 5 device copies of 512 MiB (a known-size kernel to calibrate HBM counters)")
     return ap.parse_args()
@@ -102,6 +104,9 @@ def main():
 
     ops.lib()
     torch.manual_seed(0)
+    if args.deltanet_only:
+        print(json.dumps({"deltanet": deltanet_extras(ops, torch, args.steps)}), flush=True)
+        return
     n, L = args.positions, args.layers
     kvt = ops.Q4_0
     print(f"[bench] filling {L} layer caches of {n} Q4_0 positions", file=sys.stderr, flush=True)
@@ -231,11 +236,11 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def deltanet_extras(ops, torch, steps, L=36):
-    """Gated DeltaNet layers (36 of them, each with its own 6.3 MB state): one decode token per layer, a 7-token
-    verify with the lazy commit of the first token (both as HIP-graph replays of the 36 layers, which is how the
+def deltanet_extras(ops, torch, steps, L=48):
+    """Gated DeltaNet layers (48 of them as in the model, each with its own 3.1 MB state): one decode token per layer,
+    a 7-token verify with the lazy commit of the first token (both as HIP-graph replays of the 36 layers, which is how the
     engine issues its decode step), and a 1024-token prefill chunk.  Algorithmic HBM bytes per decode
-    layer: the state read and written (2 x 48 x 128 x 128 x 4) plus the conv window, weights and token rows."""
+    layer: the state read and written (2 x 48 x 128 x 128 x 4) plus the conv window, conv weights and the token's rows."""
     ch, vd, vh = ops.DN_CH, ops.DN_VD, ops.DN_VH
     g = torch.Generator(device="cuda").manual_seed(5)
     rn = lambda *s, sc=1.0: torch.randn(*s, device="cuda", generator=g) * sc

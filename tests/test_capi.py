@@ -124,7 +124,7 @@ int main() {
     void (*dr)(const DeltaNetParams&, const float*, const float*, const float*, const float*, int, int, float, void*,
                float*, __half*, hipStream_t) = deltanet_rows;
     DNTokens tk;
-    if (dn_work_bytes(1024) != (size_t)1024 * (10240 + 2 * 2048 + 2 * 48) * 4 || tk.qkv_split != (1 << 30)) return 4;
+    if (dn_work_bytes(1024) != (size_t)1024 * (10240 + 2 * 2048 + 2 * 48 + 16) * 4 || tk.qkv_split != (1 << 30)) return 4;
     return (fp && pp && ph && ds && dm && dr) ? 0 : 3;
 }
 '''
