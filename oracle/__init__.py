@@ -73,6 +73,13 @@ def lib():
     L.qwo_max_threads.restype = ctypes.c_int
     L.qwo_deltanet.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p, _f32p,
                                ctypes.c_float, _f32p, _f32p, _f32p]
+    L.qwo_w_row_bytes.restype = ctypes.c_size_t
+    L.qwo_w_row_bytes.argtypes = [ctypes.c_int, _i64]
+    L.qwo_w_dequant_row.restype = ctypes.c_int
+    L.qwo_w_dequant_row.argtypes = [ctypes.c_int, _u8p, _f32p, _i64]
+    L.qwo_gemv_ref.restype = ctypes.c_int
+    L.qwo_gemv_ref.argtypes = [ctypes.c_int, _u8p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, _i8p, _f32p,
+                               ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
     _lib = L
     return L
 
@@ -247,3 +254,34 @@ def deltanet(qkv, z, b, a, conv_w, dt_bias, ssm_a, ssm_norm, eps, conv_state, S)
 
 def max_threads() -> int:
     return int(lib().qwo_max_threads())
+
+
+# ---- weight formats of the output-projection consumer (src/quant/quant_ref.cpp:24-101,281-299) ----
+W_Q2_K, W_Q4_K, W_Q6_K, W_IQ4_XS, W_BF16 = 10, 12, 14, 23, 30
+
+
+def w_row_bytes(fmt: int, K: int) -> int:
+    return int(lib().qwo_w_row_bytes(fmt, K))
+
+
+def w_dequant(fmt: int, W, K: int) -> np.ndarray:
+    """Rows of ggml-format weights (uint8 [N][row_bytes]) -> fp32 [N][K]."""
+    rb = w_row_bytes(fmt, K)
+    assert rb > 0
+    W = np.ascontiguousarray(W, dtype=np.uint8).reshape(-1, rb)
+    out = np.empty((W.shape[0], K), np.float32)
+    for r in range(W.shape[0]):
+        assert lib().qwo_w_dequant_row(fmt, W[r], out[r], K) == 0
+    return out
+
+
+def gemv_ref(fmt: int, W, K: int, N: int, q, d) -> np.ndarray:
+    """float64 y [nc][N] = dequant(W) . (d q) for ActQ8 columns q [nc][K], d [nc][K / 32]."""
+    rb = w_row_bytes(fmt, K)
+    q = np.ascontiguousarray(q, dtype=np.int8).reshape(-1, K)
+    d = _f32(d).reshape(q.shape[0], K // 32)
+    y = np.empty((q.shape[0], N), np.float64)
+    W = np.ascontiguousarray(W, dtype=np.uint8).reshape(-1)
+    assert lib().qwo_gemv_ref(fmt, W, rb, K, N, q.reshape(-1), d.reshape(-1), q.shape[0],
+                              y.ctypes.data_as(ctypes.POINTER(ctypes.c_double))) == 0
+    return y

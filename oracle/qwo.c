@@ -494,3 +494,131 @@ void qwo_deltanet(const float* qkv, const float* z, const float* b, const float*
     free(qn);
     free(kn);
 }
+
+
+/* ---- Weight formats (src/quant/quant_ref.cpp:24-33, 35-101, 281-299; ggml's block layouts) ---------------------
+ * Every value is formed as in the reference's scalar code (float products and differences in the same order, no FMA
+ * contraction), so that a fp16 rounding of it is the reference's prefill dequantizer output bit for bit. */
+static float w_h(const uint8_t* p) { return qwo_fp16_to_fp32((uint16_t)(p[0] | (p[1] << 8))); }
+
+size_t qwo_w_row_bytes(int fmt, int64_t K) {
+    if (fmt == QWO_W_BF16) return (size_t)K * 2;
+    if (K % 256) return 0;
+    const int64_t nb = K / 256;
+    switch (fmt) {
+        case QWO_W_Q2_K: return (size_t)nb * 84;
+        case QWO_W_Q4_K: return (size_t)nb * 144;
+        case QWO_W_Q6_K: return (size_t)nb * 210;
+        case QWO_W_IQ4_XS: return (size_t)nb * 136;
+        default: return 0;
+    }
+}
+
+/* the 6-bit scale / min pair j of a Q4_K block (12 bytes pack 8 pairs) */
+static void w_q4k_scale_min(const uint8_t* sc, int j, int* s, int* m) {
+    if (j < 4) {
+        *s = sc[j] & 63;
+        *m = sc[j + 4] & 63;
+    } else {
+        *s = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4);
+        *m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+    }
+}
+
+static const int8_t w_iq4_levels[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+int qwo_w_dequant_row(int fmt, const uint8_t* row, float* y, int64_t K) {
+    if (qwo_w_row_bytes(fmt, K) == 0) return -1;
+    if (fmt == QWO_W_BF16) {
+        for (int64_t k = 0; k < K; k++) {
+            const uint32_t bits = (uint32_t)(row[2 * k] | (row[2 * k + 1] << 8)) << 16;
+            memcpy(&y[k], &bits, 4);
+        }
+        return 0;
+    }
+    for (int64_t b = 0; b < K / 256; b++) {
+        float* out = y + 256 * b;
+        if (fmt == QWO_W_Q2_K) { /* scales[16] | qs[64] | d | dmin: 16 groups of 16, 2-bit codes */
+            const uint8_t* blk = row + 84 * b;
+            const uint8_t* sc = blk;
+            const uint8_t* qs = blk + 16;
+            const float d = w_h(blk + 80), dmin = w_h(blk + 82);
+            for (int g = 0; g < 16; g++) {
+                /* group g: weights 16 g .. 16 g + 15 = half (g & 1) of 32-byte column (g >> 3), bit pair (g >> 1) & 3 */
+                const int half = g & 1, shift = 2 * ((g >> 1) & 3), col = g >> 3;
+                const float dl = d * (float)(sc[g] & 15), ml = dmin * (float)(sc[g] >> 4);
+                for (int l = 0; l < 16; l++) {
+                    const int code = (qs[32 * col + 16 * half + l] >> shift) & 3;
+                    out[16 * g + l] = dl * (float)code - ml;
+                }
+            }
+        } else if (fmt == QWO_W_Q4_K) { /* d | dmin | scales[12] | qs[128]: 8 sub-blocks of 32, 4-bit codes */
+            const uint8_t* blk = row + 144 * b;
+            const float d = w_h(blk), dmin = w_h(blk + 2);
+            const uint8_t* sc = blk + 4;
+            const uint8_t* qs = blk + 16;
+            for (int j = 0; j < 8; j++) {
+                int s6, m6;
+                w_q4k_scale_min(sc, j, &s6, &m6);
+                const float dl = d * (float)s6, ml = dmin * (float)m6;
+                /* sub-block j: bytes 32 (j >> 1) .. + 31, low nibbles for even j, high for odd */
+                for (int l = 0; l < 32; l++) {
+                    const uint8_t byte = qs[32 * (j >> 1) + l];
+                    const int code = (j & 1) ? byte >> 4 : byte & 15;
+                    out[32 * j + l] = dl * (float)code - ml;
+                }
+            }
+        } else if (fmt == QWO_W_Q6_K) { /* ql[128] | qh[64] | scales[16] (int8) | d: 16 groups of 16, 6-bit codes */
+            const uint8_t* blk = row + 210 * b;
+            const uint8_t* ql = blk;
+            const uint8_t* qh = blk + 128;
+            const int8_t* sc = (const int8_t*)(blk + 192);
+            const float d = w_h(blk + 208);
+            for (int k = 0; k < 256; k++) {
+                /* weight k: half h = k / 128, quarter r = (k % 128) / 32, lane l = k % 32 */
+                const int h = k >> 7, r = (k >> 5) & 3, l = k & 31;
+                const uint8_t lo = ql[64 * h + 32 * (r & 1) + l];
+                const int low4 = (r & 2) ? lo >> 4 : lo & 15;
+                const int high2 = (qh[32 * h + l] >> (2 * r)) & 3;
+                const int code = (low4 | (high2 << 4)) - 32;
+                out[k] = d * (float)sc[8 * h + 2 * r + l / 16] * (float)code;
+            }
+        } else { /* IQ4_XS: d | scales_h (u16) | scales_l[4] | qs[128]: 8 sub-blocks of 32, 4-bit level indices */
+            const uint8_t* blk = row + 136 * b;
+            const float d = w_h(blk);
+            const unsigned sh = (unsigned)(blk[2] | (blk[3] << 8));
+            const uint8_t* sl = blk + 4;
+            const uint8_t* qs = blk + 8;
+            for (int j = 0; j < 8; j++) {
+                const int ls = ((sl[j / 2] >> (4 * (j % 2))) & 15) | (((sh >> (2 * j)) & 3) << 4);
+                const float dl = d * (float)(ls - 32);
+                for (int l = 0; l < 16; l++) {
+                    const uint8_t byte = qs[16 * j + l];
+                    out[32 * j + l] = dl * (float)w_iq4_levels[byte & 15];
+                    out[32 * j + 16 + l] = dl * (float)w_iq4_levels[byte >> 4];
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+int qwo_gemv_ref(int fmt, const uint8_t* W, size_t row_bytes, int K, int N, const int8_t* q, const float* d, int nc,
+                 double* y) {
+    if (qwo_w_row_bytes(fmt, K) == 0) return -1;
+    int bad = 0;
+#pragma omp parallel for schedule(static) reduction(+ : bad)
+    for (int r = 0; r < N; r++) {
+        float* w = (float*)malloc((size_t)K * sizeof(float));
+        if (!w) { bad++; continue; }
+        qwo_w_dequant_row(fmt, W + (size_t)r * row_bytes, w, K);
+        for (int c = 0; c < nc; c++) {
+            double acc = 0.0;
+            for (int k = 0; k < K; k++)
+                acc += (double)w[k] * ((double)d[(size_t)c * (K / 32) + k / 32] * (double)q[(size_t)c * K + k]);
+            y[(size_t)c * N + r] = acc;
+        }
+        free(w);
+    }
+    return bad ? -2 : 0;
+}

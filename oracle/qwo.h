@@ -87,6 +87,19 @@ void qwo_deltanet(const float* qkv, const float* z, const float* b, const float*
                   const float* conv_w, const float* dt_bias, const float* ssm_a, const float* ssm_norm, float eps,
                   float* conv_state, float* S, float* o);
 
+/* Weight formats of the output-projection consumer (decode GEMV over ActQ8 activations, prefill fp16 dequant):
+ * ggml block layouts of src/quant/quant_formats.h:92-104, 256 weights per block.  Format ids are the reference's
+ * QuantFormat values (include/q38rt/q38rt_types.h:36-66). */
+enum { QWO_W_Q2_K = 10, QWO_W_Q4_K = 12, QWO_W_Q6_K = 14, QWO_W_IQ4_XS = 23, QWO_W_BF16 = 30 };
+/* bytes of one row of K weights (0 for an unsupported format or K not a multiple of the block) */
+size_t qwo_w_row_bytes(int fmt, int64_t K);
+/* dequantize one row of K weights to fp32; 0 on success, -1 for an unsupported format */
+int qwo_w_dequant_row(int fmt, const uint8_t* row, float* y, int64_t K);
+/* y[c][r] = sum_k dequant(W[r])[k] * d_c[k / 32] * q_c[k] in double, for nc activation columns (q [nc][K],
+ * d [nc][K / 32]); the decode GEMV's exact target (tests/kernels/test_gemv.cu:69-92) */
+int qwo_gemv_ref(int fmt, const uint8_t* W, size_t row_bytes, int K, int N, const int8_t* q, const float* d, int nc,
+                 double* y);
+
 #ifdef __cplusplus
 }
 #endif
