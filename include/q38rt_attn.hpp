@@ -215,5 +215,51 @@ inline void deltanet_rows(const DeltaNetParams& p, const float* qkv, const float
                   "deltanet_rows");
 }
 
+// ---- consumers of the attention output (src/cuda/gemv.cuh:20-39, src/cuda/prefill.cuh:16-18).  The format argument
+// is the engine's QuantFormat (include/q38rt/q38rt_types.h:36-66), taken as any enum whose values are the format ids.
+// Like the reference these return false for a format without a kernel; other rejected arguments abort.
+template <class QF>
+inline bool gemv_q8_supported(QF type) {
+    return qwa_gemv_q8_supported(static_cast<int>(type)) != 0;
+}
+
+inline void quantize_act_q8(const float* x, int K, int n_rows, ActQ8 out, hipStream_t st) {
+    const qwa_act_q8 q8{out.q, out.d, out.s};
+    detail::check(qwa_quantize_act_q8(x, K, n_rows, &q8, st), "quantize_act_q8");
+}
+
+template <class QF>
+inline bool gemv_q8(QF type, const void* W, size_t row_bytes, int K, int N, const ActQ8& act, float* y, hipStream_t st,
+                    bool accumulate = false) {
+    if (!gemv_q8_supported(type)) return false;
+    const qwa_act_q8 q8{act.q, act.d, act.s};
+    detail::check(qwa_gemv_q8(static_cast<int>(type), W, row_bytes, K, N, &q8, y, st, accumulate ? 1 : 0), "gemv_q8");
+    return true;
+}
+
+template <class QF>
+inline bool gemv_q8n(QF type, const void* W, size_t row_bytes, int K, int N, const ActQ8& act, int nb, int act_ld,
+                     float* y, int y_ld, hipStream_t st, bool accumulate = false) {
+    if (!gemv_q8_supported(type)) return false;
+    const qwa_act_q8 q8{act.q, act.d, act.s};
+    detail::check(qwa_gemv_q8n(static_cast<int>(type), W, row_bytes, K, N, &q8, nb, act_ld, y, y_ld, st,
+                               accumulate ? 1 : 0),
+                  "gemv_q8n");
+    return true;
+}
+
+inline void gemv_bf16(const uint16_t* W, int K, int N, const float* x, float* y, hipStream_t st) {
+    detail::check(qwa_gemv_bf16(W, K, N, x, y, st), "gemv_bf16");
+}
+
+template <class QF>
+inline bool dequant_rows_f16(QF type, const void* W, size_t row_bytes, int K, int rows, __half* out, hipStream_t st) {
+    if (qwa_w_row_bytes(static_cast<int>(type), K) == 0) return false;
+    detail::check(qwa_dequant_rows_f16(static_cast<int>(type), W, row_bytes, K, rows, reinterpret_cast<uint16_t*>(out),
+                                       st),
+                  "dequant_rows_f16");
+    return true;
+}
+
 }  // namespace cuda
 }  // namespace q38rt

@@ -199,6 +199,43 @@ int qwa_deltanet_rows(const qwa_dn_params* p, const float* qkv, const float* z, 
                       const float* alpha_raw, int B, int cin, float eps, void* work, float* core_out, uint16_t* o16,
                       void* stream);
 
+/* ---- Consumers of the attention output: decode GEMV over ActQ8 activations, prefill weight dequantizer --------- */
+
+/* Weight formats, the reference's QuantFormat values (include/q38rt/q38rt_types.h:36-66), ggml block layouts
+ * (src/quant/quant_formats.h:92-104).  The grid formats (IQ1_S / IQ1_M / IQ2_* / IQ3_*) are not supported here. */
+#define QWA_W_Q2_K 10
+#define QWA_W_Q4_K 12
+#define QWA_W_Q6_K 14
+#define QWA_W_IQ4_XS 23
+#define QWA_W_BF16 30
+
+/* Bytes of one row of K weights in format fmt (0: unsupported format, or K not a multiple of the 256-weight block). */
+size_t qwa_w_row_bytes(int fmt, long long K);
+
+/* Replaces gemv_q8_supported (src/cuda/gemv.cuh:38-39): 1 if qwa_gemv_q8 has a kernel for fmt. */
+int qwa_gemv_q8_supported(int fmt);
+
+/* Replaces quantize_act_q8 (src/cuda/gemv.cuh:20-21): n_rows rows of K fp32 values (stride K) into ActQ8 (same
+ * layout; d = amax / 127, q = round-half-even(x / d), s = d * sum(q) per 32 values).  K a multiple of 32. */
+int qwa_quantize_act_q8(const float* x, int K, int n_rows, const qwa_act_q8* out, void* stream);
+
+/* Replaces gemv_q8 (src/cuda/gemv.cuh:23-27): y[r] (+)= W[r, :] . act for r < N; W row-major, row_bytes apart, in
+ * format fmt with K weights per row (K a multiple of 256).  QWA_ERR_INVALID for a format without a kernel. */
+int qwa_gemv_q8(int fmt, const void* W, size_t row_bytes, int K, int N, const qwa_act_q8* act, float* y, void* stream,
+                int accumulate);
+
+/* Replaces gemv_q8n (src/cuda/gemv.cuh:33-36): nb (1..4) activation columns at act->q + c * act_ld (d / s at
+ * + c * act_ld / 32); y[c * y_ld + r] (+)= W[r, :] . x_c.  Each column's result is bit-identical to qwa_gemv_q8 on it. */
+int qwa_gemv_q8n(int fmt, const void* W, size_t row_bytes, int K, int N, const qwa_act_q8* act, int nb, int act_ld,
+                 float* y, int y_ld, void* stream, int accumulate);
+
+/* Replaces gemv_bf16 (src/cuda/gemv.cuh:29-30): y[r] = W[r, :] . x for BF16 weights [N][K] (K a multiple of 8). */
+int qwa_gemv_bf16(const uint16_t* W, int K, int N, const float* x, float* y, void* stream);
+
+/* Replaces dequant_rows_f16 (src/cuda/prefill.cuh:16-18): rows of K weights to fp16 [rows][K]; each value is the
+ * reference dequantizer's fp32 value rounded to fp16 (nearest-even).  BF16 rows are accepted (row_bytes = 2 K). */
+int qwa_dequant_rows_f16(int fmt, const void* W, size_t row_bytes, int K, int rows, uint16_t* out, void* stream);
+
 /* Opt-in kernel timing (no reference counterpart; the reference times phases with env-gated GPU timers,
  * src/runtime/engine.cpp:2477-2480): between qwa_profile_begin() and qwa_profile_end(), every launch of an
  * attention call's main kernel (decode: the split-K kernel; prefill: the MFMA kernel) is bracketed by two HIP events

@@ -16,7 +16,8 @@ OUT_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(OUT_DIR, "libqwattn.so")
 ARCH = "gfx950"
 
-SOURCES = ["capi.hip", "kv_append.hip", "attn_decode.hip", "attn_simple.hip", "attn_prefill.hip", "deltanet.hip"]
+SOURCES = ["capi.hip", "kv_append.hip", "attn_decode.hip", "attn_simple.hip", "attn_prefill.hip", "deltanet.hip",
+           "gemv.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

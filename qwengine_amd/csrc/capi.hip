@@ -331,6 +331,59 @@ int qwa_deltanet_rows(const qwa_dn_params* p, const float* qkv, const float* z, 
                     fn);
 }
 
+// ---- consumers of the attention output (gemv.hip)
+size_t qwa_w_row_bytes(int fmt, long long K) { return qwa::w_row_bytes(fmt, K); }
+
+int qwa_gemv_q8_supported(int fmt) { return qwa::gemv_q8_supported(fmt) ? 1 : 0; }
+
+int qwa_quantize_act_q8(const float* x, int K, int n_rows, const qwa_act_q8* out, void* stream) {
+    const char* fn = "quantize_act_q8";
+    if (K <= 0 || K % 32 || n_rows <= 0) return fail(QWA_ERR_RANGE, "%s: K = %d, n_rows = %d", fn, K, n_rows);
+    if (!x || !out || !out->q || !out->d || !out->s) return fail(QWA_ERR_INVALID, "%s: missing buffer", fn);
+    if ((long long)K * n_rows / 32 > 8LL * 65535 * 1024) return fail(QWA_ERR_RANGE, "%s: too many values", fn);
+    return from_hip(qwa::launch_act_q8(x, (long long)K * n_rows, *out, as_stream(stream)), fn);
+}
+
+int qwa_gemv_q8n(int fmt, const void* W, size_t row_bytes, int K, int N, const qwa_act_q8* act, int nb, int act_ld,
+                 float* y, int y_ld, void* stream, int accumulate) {
+    const char* fn = "gemv_q8";
+    if (!qwa::gemv_q8_supported(fmt)) return fail(QWA_ERR_INVALID, "%s: no kernel for weight format %d", fn, fmt);
+    if (K <= 0 || K % 256 || N <= 0) return fail(QWA_ERR_RANGE, "%s: K = %d, N = %d", fn, K, N);
+    if (row_bytes < qwa::w_row_bytes(fmt, K))
+        return fail(QWA_ERR_RANGE, "%s: row_bytes %zu < %zu", fn, row_bytes, qwa::w_row_bytes(fmt, K));
+    if (nb < 1 || nb > 4) return fail(QWA_ERR_RANGE, "%s: %d columns (1..4)", fn, nb);
+    if (nb > 1 && (act_ld < K || act_ld % 32)) return fail(QWA_ERR_RANGE, "%s: act_ld %d", fn, act_ld);
+    if (nb > 1 && y_ld < N) return fail(QWA_ERR_RANGE, "%s: y_ld %d < N %d", fn, y_ld, N);
+    if (!W || !act || !act->q || !act->d || !act->s || !y) return fail(QWA_ERR_INVALID, "%s: missing buffer", fn);
+    return from_hip(qwa::launch_gemv_q8(fmt, W, row_bytes, K, N, *act, nb, nb > 1 ? act_ld : K, y, nb > 1 ? y_ld : N,
+                                        accumulate ? 1 : 0, as_stream(stream)),
+                    fn);
+}
+
+int qwa_gemv_q8(int fmt, const void* W, size_t row_bytes, int K, int N, const qwa_act_q8* act, float* y, void* stream,
+                int accumulate) {
+    return qwa_gemv_q8n(fmt, W, row_bytes, K, N, act, 1, K, y, N, stream, accumulate);
+}
+
+int qwa_gemv_bf16(const uint16_t* W, int K, int N, const float* x, float* y, void* stream) {
+    const char* fn = "gemv_bf16";
+    if (K <= 0 || K % 8 || N <= 0) return fail(QWA_ERR_RANGE, "%s: K = %d, N = %d", fn, K, N);
+    if (!W || !x || !y) return fail(QWA_ERR_INVALID, "%s: missing buffer", fn);
+    return from_hip(qwa::launch_gemv_bf16(W, K, N, x, y, as_stream(stream)), fn);
+}
+
+int qwa_dequant_rows_f16(int fmt, const void* W, size_t row_bytes, int K, int rows, uint16_t* out, void* stream) {
+    const char* fn = "dequant_rows_f16";
+    if (qwa::w_row_bytes(fmt, K) == 0) return fail(QWA_ERR_INVALID, "%s: weight format %d, K = %d", fn, fmt, K);
+    if (rows <= 0) return fail(QWA_ERR_RANGE, "%s: rows = %d", fn, rows);
+    if (row_bytes < qwa::w_row_bytes(fmt, K))
+        return fail(QWA_ERR_RANGE, "%s: row_bytes %zu < %zu", fn, row_bytes, qwa::w_row_bytes(fmt, K));
+    if (fmt == QWA_W_BF16 && row_bytes != (size_t)K * 2)
+        return fail(QWA_ERR_RANGE, "%s: BF16 rows must be contiguous (row_bytes = 2 K)", fn);
+    if (!W || !out) return fail(QWA_ERR_INVALID, "%s: missing buffer", fn);
+    return from_hip(qwa::launch_dequant_f16(fmt, W, row_bytes, K, rows, out, as_stream(stream)), fn);
+}
+
 int qwa_profile_begin(void) {
     const size_t bytes = (size_t)PROF_MAX * qwa::PROF_MAX_WG * 2 * sizeof(unsigned long long);
     if (g_prof.stamps == nullptr) {

@@ -1,0 +1,374 @@
+// The consumers of the attention output (gfx950): the decode GEMV over ActQ8 activations, the activation quantizer,
+// the BF16 GEMV of the small projections and the prefill dequantizer of weight rows to fp16.
+//
+// Decode GEMV: y[c][r] (+)= W[r, :] . x_c for up to 4 activation columns x_c = d_c * q_c (int8 per 32 values,
+// src/cuda/gemv.cuh:12-36).  One wave per weight row (grid-stride); lane u takes the 32-weight sub-blocks u, u + 64,
+// ... of the row.  A sub-block is decoded once into 8 dwords of int8 codes plus its group scales / mins, dotted with
+// every column by v_dot4_i32_i8, and scaled in fp32:
+//     sum_k W x = d_x (g0 . i0 + g1 . i1) - (m0 . q0 + m1 . q1) d_x
+// (i = integer dot of the codes with the activation bytes over a 16-weight group, q = sum of the activation bytes
+// of the group, g / m = the group's scale / min).  Weight bytes stream once through HBM; the activations (a few KB)
+// stay in L1 / L2.  A column's result does not depend on how many columns share the call.
+//
+// Formats (ggml layouts of src/quant/quant_formats.h:92-104): Q2_K, Q4_K, Q6_K, IQ4_XS; BF16 through gemv_bf16 and
+// the dequantizer.  The IQ1 / IQ2 / IQ3 grid formats are not built (their codebooks are not part of this library).
+#include "launch.hpp"
+#include "qwattn_common.hpp"
+
+namespace qwa {
+
+constexpr int GV_WAVES = 8;  // rows (waves) per workgroup
+
+__device__ __forceinline__ float gv_h(const uint8_t* p) {
+    return h2f_bits((uint16_t)(p[0] | ((uint16_t)p[1] << 8)));
+}
+__device__ __forceinline__ uint32_t gv_u32(const uint8_t* p) {  // 4-byte aligned
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+__device__ __forceinline__ uint32_t gv_u32_a2(const uint8_t* p) {  // 2-byte aligned (Q6_K blocks are 210 bytes)
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+    return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+}
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// A decoded 32-weight sub-block: int8 codes (natural order) and per-16-weight scale / min.  Weight k of group h
+// (k = 16 h + l) is g_h * code_k - m_h, with code_k = c[k / 4] byte k % 4 minus `bias`.
+struct WSub {
+    uint32_t c[8];
+    float g0, g1, m0, m1;
+};
+
+template <int FMT> struct WFmt;
+
+template <> struct WFmt<QWA_W_Q4_K> {  // d | dmin | scales[12] | qs[128]
+    static constexpr int BYTES = 144, BIAS = 0;
+    static constexpr bool HALVES = false, MINS = true;
+    __device__ static void sub(const uint8_t* b, int j, WSub& w) {
+        const float d = gv_h(b), dmin = gv_h(b + 2);
+        const uint32_t s0 = gv_u32(b + 4), s1 = gv_u32(b + 8), s2 = gv_u32(b + 12);
+        const uint8_t sc[12] = {(uint8_t)s0, (uint8_t)(s0 >> 8), (uint8_t)(s0 >> 16), (uint8_t)(s0 >> 24),
+                                (uint8_t)s1, (uint8_t)(s1 >> 8), (uint8_t)(s1 >> 16), (uint8_t)(s1 >> 24),
+                                (uint8_t)s2, (uint8_t)(s2 >> 8), (uint8_t)(s2 >> 16), (uint8_t)(s2 >> 24)};
+        int s6, m6;
+        if (j < 4) {
+            s6 = sc[j] & 63;
+            m6 = sc[j + 4] & 63;
+        } else {
+            s6 = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4);
+            m6 = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+        }
+        const uint4* q = reinterpret_cast<const uint4*>(b + 16 + 32 * (j >> 1));
+        const uint4 a = q[0], bb = q[1];
+        const uint32_t raw[8] = {a.x, a.y, a.z, a.w, bb.x, bb.y, bb.z, bb.w};
+        const int sh = 4 * (j & 1);
+#pragma unroll
+        for (int i = 0; i < 8; i++) w.c[i] = (raw[i] >> sh) & 0x0F0F0F0Fu;
+        w.g0 = w.g1 = d * (float)s6;
+        w.m0 = w.m1 = dmin * (float)m6;
+    }
+};
+
+template <> struct WFmt<QWA_W_Q2_K> {  // scales[16] | qs[64] | d | dmin
+    static constexpr int BYTES = 84, BIAS = 0;
+    static constexpr bool HALVES = true, MINS = true;
+    __device__ static void sub(const uint8_t* b, int j, WSub& w) {
+        const uint32_t dd = gv_u32(b + 80);
+        const float d = h2f_bits((uint16_t)dd), dmin = h2f_bits((uint16_t)(dd >> 16));
+        const uint32_t scw = gv_u32(b + 4 * (j >> 1));
+        const uint32_t sa = (scw >> (16 * (j & 1))) & 0xFF, sb = (scw >> (16 * (j & 1) + 8)) & 0xFF;
+        const uint8_t* q = b + 16 + 32 * (j >> 2);
+        const int sh = 2 * (j & 3);
+#pragma unroll
+        for (int i = 0; i < 8; i++) w.c[i] = (gv_u32(q + 4 * i) >> sh) & 0x03030303u;
+        w.g0 = d * (float)(sa & 15);
+        w.m0 = dmin * (float)(sa >> 4);
+        w.g1 = d * (float)(sb & 15);
+        w.m1 = dmin * (float)(sb >> 4);
+    }
+};
+
+template <> struct WFmt<QWA_W_Q6_K> {  // ql[128] | qh[64] | scales[16] (int8) | d
+    static constexpr int BYTES = 210, BIAS = 32;
+    static constexpr bool HALVES = true, MINS = false;
+    __device__ static void sub(const uint8_t* b, int j, WSub& w) {
+        const int h = j >> 2, r = j & 3;
+        const float d = gv_h(b + 208);
+        const uint8_t* ql = b + 64 * h + 32 * (r & 1);
+        const uint8_t* qh = b + 128 + 32 * h;
+        const int sl = 4 * (r >> 1), sh = 2 * r;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t lo = (gv_u32_a2(ql + 4 * i) >> sl) & 0x0F0F0F0Fu;
+            const uint32_t hi = ((gv_u32_a2(qh + 4 * i) >> sh) & 0x03030303u) << 4;
+            w.c[i] = lo | hi;  // 0 .. 63; the bias 32 is taken off through the activation sums
+        }
+        const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + 8 * h + 2 * r);
+        w.g0 = d * (float)sc[0];
+        w.g1 = d * (float)sc[1];
+        w.m0 = w.m1 = 0.0f;
+    }
+};
+
+template <> struct WFmt<QWA_W_IQ4_XS> {  // d | scales_h (u16) | scales_l[4] | qs[128]
+    static constexpr int BYTES = 136, BIAS = 0;
+    static constexpr bool HALVES = false, MINS = false;
+    // the 16 non-uniform levels as four little-endian dwords (ggml's kvalues_iq4nl, src/quant/iq_tables.inc:373-375)
+    static constexpr uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
+    __device__ static uint32_t levels(uint32_t nib) {  // four nibble indices (one per byte) -> four int8 levels
+        const uint32_t sel = nib & 0x07070707u;
+        const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+        const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
+        return (hi & m) | (lo & ~m);
+    }
+    __device__ static void sub(const uint8_t* b, int j, WSub& w) {
+        const uint32_t hdr = gv_u32(b), sl = gv_u32(b + 4);
+        const float d = h2f_bits((uint16_t)hdr);
+        const uint32_t shi = hdr >> 16;
+        const int ls = (int)(((sl >> (8 * (j >> 1) + 4 * (j & 1))) & 15) | (((shi >> (2 * j)) & 3) << 4));
+        const uint4 q = *reinterpret_cast<const uint4*>(b + 8 + 16 * j);
+        const uint32_t raw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w.c[i] = levels(raw[i] & 0x0F0F0F0Fu);
+            w.c[4 + i] = levels((raw[i] >> 4) & 0x0F0F0F0Fu);
+        }
+        w.g0 = w.g1 = d * (float)(ls - 32);
+        w.m0 = w.m1 = 0.0f;
+    }
+};
+
+// One wave per row; NB activation columns at aq + c * act_ld (d / s at + c * act_ld / 32)
+template <int FMT, int NB>
+__global__ void __launch_bounds__(GV_WAVES * 64) k_gemv_q8(const uint8_t* __restrict__ W, size_t row_bytes, int K,
+                                                           int N, const int8_t* __restrict__ aq,
+                                                           const float* __restrict__ ad, const float* __restrict__ as,
+                                                           int act_ld, float* __restrict__ y, int y_ld,
+                                                           int accumulate) {
+    using F = WFmt<FMT>;
+    const int lane = threadIdx.x & 63;
+    const int nsub = K / 32;
+    const uint32_t ones = 0x01010101u;
+    for (int row = blockIdx.x * GV_WAVES + (int)(threadIdx.x >> 6); row < N; row += gridDim.x * GV_WAVES) {
+        const uint8_t* wr = W + (size_t)row * row_bytes;
+        float acc[NB];
+#pragma unroll
+        for (int c = 0; c < NB; c++) acc[c] = 0.0f;
+        for (int u = lane; u < nsub; u += 64) {
+            WSub w;
+            F::sub(wr + (size_t)(u >> 3) * F::BYTES, u & 7, w);
+#pragma unroll
+            for (int c = 0; c < NB; c++) {
+                const uint4* xp = reinterpret_cast<const uint4*>(aq + (size_t)c * act_ld + 32 * u);
+                const uint4 x0 = xp[0], x1 = xp[1];
+                const float dx = ad[(size_t)c * (act_ld / 32) + u];
+                int i0 = dot4(w.c[0], x0.x, dot4(w.c[1], x0.y, dot4(w.c[2], x0.z, dot4(w.c[3], x0.w, 0))));
+                int i1 = dot4(w.c[4], x1.x, dot4(w.c[5], x1.y, dot4(w.c[6], x1.z, dot4(w.c[7], x1.w, 0))));
+                if constexpr (F::HALVES) {
+                    const int q0 = dot4(ones, x0.x, dot4(ones, x0.y, dot4(ones, x0.z, dot4(ones, x0.w, 0))));
+                    const int q1 = dot4(ones, x1.x, dot4(ones, x1.y, dot4(ones, x1.z, dot4(ones, x1.w, 0))));
+                    if constexpr (F::BIAS != 0) {
+                        i0 -= F::BIAS * q0;
+                        i1 -= F::BIAS * q1;
+                    }
+                    float v = w.g0 * (float)i0 + w.g1 * (float)i1;
+                    if constexpr (F::MINS) v -= w.m0 * (float)q0 + w.m1 * (float)q1;
+                    acc[c] = fmaf(dx, v, acc[c]);
+                } else {
+                    acc[c] = fmaf(dx * w.g0, (float)(i0 + i1), acc[c]);
+                    if constexpr (F::MINS) acc[c] = fmaf(-w.m0, as[(size_t)c * (act_ld / 32) + u], acc[c]);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            const float v = wave_sum(acc[c]);
+            if (lane == 0) {
+                float* yo = y + (size_t)c * y_ld + row;
+                *yo = accumulate ? *yo + v : v;
+            }
+        }
+    }
+}
+
+// ActQ8 of n_rows rows of K values (stride K): one 32-lane half-wave per 32-value block (src/cuda/gemv.cu:30-46)
+__global__ void __launch_bounds__(256) k_act_q8_rows(const float* __restrict__ x, int n_blocks, int8_t* __restrict__ q,
+                                                     float* __restrict__ d, float* __restrict__ s) {
+    const int blk = blockIdx.x * 8 + (int)(threadIdx.x >> 5), l = threadIdx.x & 31;
+    const bool on = blk < n_blocks;
+    const float v = on ? x[(size_t)blk * 32 + l] : 0.0f;
+    const float amax = half_max(fabsf(v));
+    const float db = amax / 127.0f;
+    const int qi = db > 0.0f ? (int)__builtin_rintf(v / db) : 0;
+    const float sum = half_sum((float)qi);
+    if (on) {
+        q[(size_t)blk * 32 + l] = (int8_t)qi;
+        if (l == 0) {
+            d[blk] = db;
+            s[blk] = db * sum;
+        }
+    }
+}
+
+// y[r] = W[r, :] . x for BF16 weights: one wave per row, 8 weights per lane and step (src/cuda/gemv.cu:125-143)
+__global__ void __launch_bounds__(256) k_gemv_bf16(const uint16_t* __restrict__ W, int K, int N,
+                                                   const float* __restrict__ x, float* __restrict__ y) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (row >= N) return;
+    const uint16_t* w = W + (size_t)row * K;
+    float acc = 0.0f;
+    for (int k = 8 * lane; k < K; k += 512) {
+        const uint4 p = *reinterpret_cast<const uint4*>(w + k);
+        const uint32_t u[4] = {p.x, p.y, p.z, p.w};
+        const float4 xa = *reinterpret_cast<const float4*>(x + k), xb = *reinterpret_cast<const float4*>(x + k + 4);
+        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            acc = fmaf(__uint_as_float(u[i] << 16), xv[2 * i], acc);
+            acc = fmaf(__uint_as_float(u[i] & 0xFFFF0000u), xv[2 * i + 1], acc);
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
+// ---- prefill: weight rows to fp16, bit-exact with fp16(RNE) of the reference dequantizer's fp32 value
+// (src/cuda/prefill.cuh:16-18).  One thread per 32-weight sub-block; values formed as the reference forms them, with
+// no FMA contraction.
+#pragma clang fp contract(off)
+template <int FMT>
+__device__ __forceinline__ void dq_sub(const uint8_t* b, int j, float* v) {
+    if constexpr (FMT == QWA_W_Q4_K) {
+        WSub w;
+        WFmt<FMT>::sub(b, j, w);
+        // w.g0 = d * s6, w.m0 = dmin * m6, as the reference's d1 / m1
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = w.g0 * (float)((w.c[i / 4] >> (8 * (i % 4))) & 0xFF) - w.m0;
+    } else if constexpr (FMT == QWA_W_Q2_K) {
+        WSub w;
+        WFmt<FMT>::sub(b, j, w);
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const float code = (float)((w.c[i / 4] >> (8 * (i % 4))) & 0xFF);
+            v[i] = i < 16 ? w.g0 * code - w.m0 : w.g1 * code - w.m1;
+        }
+    } else if constexpr (FMT == QWA_W_Q6_K) {
+        WSub w;
+        WFmt<FMT>::sub(b, j, w);
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const float code = (float)((int)((w.c[i / 4] >> (8 * (i % 4))) & 0xFF) - 32);
+            v[i] = (i < 16 ? w.g0 : w.g1) * code;
+        }
+    } else {  // IQ4_XS
+        WSub w;
+        WFmt<FMT>::sub(b, j, w);
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = w.g0 * (float)(int8_t)((w.c[i / 4] >> (8 * (i % 4))) & 0xFF);
+    }
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(256) k_dequant_f16(const uint8_t* __restrict__ W, size_t row_bytes, int K, int rows,
+                                                     uint16_t* __restrict__ out) {
+    const int nsub = K / 32;
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long long)rows * nsub) return;
+    const int r = (int)(i / nsub), u = (int)(i % nsub);
+    float v[32];
+    dq_sub<FMT>(W + (size_t)r * row_bytes + (size_t)(u >> 3) * WFmt<FMT>::BYTES, u & 7, v);
+    // the fp32 values stay opaque to the conversion: otherwise a product and its fp16 rounding fold into one
+    // mixed-precision fma with a +0 addend, which turns -0 into +0
+#pragma unroll
+    for (int k = 0; k < 32; k++) asm volatile("" : "+v"(v[k]));
+    uint32_t h[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) h[k] = (uint32_t)f2h_bits(v[2 * k]) | ((uint32_t)f2h_bits(v[2 * k + 1]) << 16);
+    uint4* dst = reinterpret_cast<uint4*>(out + (size_t)r * K + 32 * u);
+#pragma unroll
+    for (int k = 0; k < 4; k++) dst[k] = make_uint4(h[4 * k], h[4 * k + 1], h[4 * k + 2], h[4 * k + 3]);
+}
+
+__global__ void __launch_bounds__(256) k_bf16_to_f16(const uint16_t* __restrict__ W, long long n,
+                                                     uint16_t* __restrict__ out) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = f2h_bits(__uint_as_float((uint32_t)W[i] << 16));
+}
+#pragma clang fp contract(on)
+
+// ------------------------------------------------------------------------------------------------------ launchers
+size_t w_row_bytes(int fmt, long long K) {
+    if (fmt == QWA_W_BF16) return (size_t)K * 2;
+    if (K <= 0 || K % 256) return 0;
+    switch (fmt) {
+        case QWA_W_Q2_K: return (size_t)(K / 256) * WFmt<QWA_W_Q2_K>::BYTES;
+        case QWA_W_Q4_K: return (size_t)(K / 256) * WFmt<QWA_W_Q4_K>::BYTES;
+        case QWA_W_Q6_K: return (size_t)(K / 256) * WFmt<QWA_W_Q6_K>::BYTES;
+        case QWA_W_IQ4_XS: return (size_t)(K / 256) * WFmt<QWA_W_IQ4_XS>::BYTES;
+        default: return 0;
+    }
+}
+
+bool gemv_q8_supported(int fmt) {
+    return fmt == QWA_W_Q2_K || fmt == QWA_W_Q4_K || fmt == QWA_W_Q6_K || fmt == QWA_W_IQ4_XS;
+}
+
+template <int FMT>
+static hipError_t gemv_fmt(const void* W, size_t rb, int K, int N, const qwa_act_q8& a, int nb, int act_ld, float* y,
+                           int y_ld, int acc, hipStream_t st) {
+    const dim3 grid((unsigned)min((N + GV_WAVES - 1) / GV_WAVES, 65535)), block(GV_WAVES * 64);
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    switch (nb) {
+        case 1: hipLaunchKernelGGL((k_gemv_q8<FMT, 1>), grid, block, 0, st, w, rb, K, N, a.q, a.d, a.s, act_ld, y, y_ld, acc); break;
+        case 2: hipLaunchKernelGGL((k_gemv_q8<FMT, 2>), grid, block, 0, st, w, rb, K, N, a.q, a.d, a.s, act_ld, y, y_ld, acc); break;
+        case 3: hipLaunchKernelGGL((k_gemv_q8<FMT, 3>), grid, block, 0, st, w, rb, K, N, a.q, a.d, a.s, act_ld, y, y_ld, acc); break;
+        default: hipLaunchKernelGGL((k_gemv_q8<FMT, 4>), grid, block, 0, st, w, rb, K, N, a.q, a.d, a.s, act_ld, y, y_ld, acc); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_q8(int fmt, const void* W, size_t rb, int K, int N, const qwa_act_q8& a, int nb, int act_ld,
+                          float* y, int y_ld, int accumulate, hipStream_t st) {
+    switch (fmt) {
+        case QWA_W_Q2_K: return gemv_fmt<QWA_W_Q2_K>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
+        case QWA_W_Q4_K: return gemv_fmt<QWA_W_Q4_K>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
+        case QWA_W_Q6_K: return gemv_fmt<QWA_W_Q6_K>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
+        case QWA_W_IQ4_XS: return gemv_fmt<QWA_W_IQ4_XS>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_act_q8(const float* x, long long n, const qwa_act_q8& out, hipStream_t st) {
+    const long long nblk = n / 32;
+    hipLaunchKernelGGL(k_act_q8_rows, dim3((unsigned)((nblk + 7) / 8)), dim3(256), 0, st, x, (int)nblk, out.q, out.d,
+                       out.s);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_bf16(const uint16_t* W, int K, int N, const float* x, float* y, hipStream_t st) {
+    hipLaunchKernelGGL(k_gemv_bf16, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, W, K, N, x, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_f16(int fmt, const void* W, size_t rb, int K, int rows, uint16_t* out, hipStream_t st) {
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    if (fmt == QWA_W_BF16) {
+        const long long n = (long long)rows * K;
+        hipLaunchKernelGGL(k_bf16_to_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           reinterpret_cast<const uint16_t*>(W), n, out);
+        return hipGetLastError();
+    }
+    const long long n = (long long)rows * (K / 32);
+    const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    switch (fmt) {
+        case QWA_W_Q2_K: hipLaunchKernelGGL(k_dequant_f16<QWA_W_Q2_K>, grid, block, 0, st, w, rb, K, rows, out); break;
+        case QWA_W_Q4_K: hipLaunchKernelGGL(k_dequant_f16<QWA_W_Q4_K>, grid, block, 0, st, w, rb, K, rows, out); break;
+        case QWA_W_Q6_K: hipLaunchKernelGGL(k_dequant_f16<QWA_W_Q6_K>, grid, block, 0, st, w, rb, K, rows, out); break;
+        case QWA_W_IQ4_XS: hipLaunchKernelGGL(k_dequant_f16<QWA_W_IQ4_XS>, grid, block, 0, st, w, rb, K, rows, out); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace qwa

@@ -60,4 +60,13 @@ hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer&
 hipError_t launch_prefill_simple(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
                                  uint16_t* out16, hipStream_t st);
 
+// gemv.hip
+size_t w_row_bytes(int fmt, long long K);
+bool gemv_q8_supported(int fmt);
+hipError_t launch_gemv_q8(int fmt, const void* W, size_t rb, int K, int N, const qwa_act_q8& a, int nb, int act_ld,
+                          float* y, int y_ld, int accumulate, hipStream_t st);
+hipError_t launch_act_q8(const float* x, long long n, const qwa_act_q8& out, hipStream_t st);
+hipError_t launch_gemv_bf16(const uint16_t* W, int K, int N, const float* x, float* y, hipStream_t st);
+hipError_t launch_dequant_f16(int fmt, const void* W, size_t rb, int K, int rows, uint16_t* out, hipStream_t st);
+
 }  // namespace qwa

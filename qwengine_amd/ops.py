@@ -98,6 +98,19 @@ EXPORTS = {
                            [ctypes.c_int] * 3 + [ctypes.c_float, ctypes.c_void_p, ctypes.POINTER(_ActQ8C),
                                                  ctypes.c_void_p]),
     "qwa_dn_work_bytes": (ctypes.c_size_t, [ctypes.c_int]),
+    "qwa_w_row_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_longlong]),
+    "qwa_gemv_q8_supported": (ctypes.c_int, [ctypes.c_int]),
+    "qwa_quantize_act_q8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_ActQ8C),
+                                           ctypes.c_void_p]),
+    "qwa_gemv_q8": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                   ctypes.POINTER(_ActQ8C), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]),
+    "qwa_gemv_q8n": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                    ctypes.POINTER(_ActQ8C), ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_int]),
+    "qwa_gemv_bf16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_void_p]),
+    "qwa_dequant_rows_f16": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]),
     "qwa_deltanet_rows": (ctypes.c_int, [ctypes.POINTER(_DNParamsC)] + [ctypes.c_void_p] * 4 +
                           [ctypes.c_int, ctypes.c_int, ctypes.c_float] + [ctypes.c_void_p] * 4),
     "qwa_profile_begin": (ctypes.c_int, []),
@@ -427,3 +440,43 @@ def deltanet_rows(p: DNParams, qkv, z, beta_raw, alpha_raw, B: int, cin: int, ep
     """src/cuda/prefill.cuh:42-44."""
     _check(lib().qwa_deltanet_rows(ctypes.byref(p.c()), _ptr(qkv), _ptr(z), _ptr(beta_raw), _ptr(alpha_raw), B, cin,
                                    eps, _ptr(work), _ptr(core_out), _ptr(o16), _stream(stream)))
+
+
+# ---- consumers of the attention output (src/cuda/gemv.cuh:20-39, src/cuda/prefill.cuh:16-18) ------------------------
+W_Q2_K, W_Q4_K, W_Q6_K, W_IQ4_XS, W_BF16 = 10, 12, 14, 23, 30
+
+
+def w_row_bytes(fmt: int, K: int) -> int:
+    return int(lib().qwa_w_row_bytes(fmt, K))
+
+
+def gemv_q8_supported(fmt: int) -> bool:
+    return bool(lib().qwa_gemv_q8_supported(fmt))
+
+
+def quantize_act_q8(x, K: int, n_rows: int, out: ActQ8, stream=None) -> None:
+    """src/cuda/gemv.cuh:20-21."""
+    _check(lib().qwa_quantize_act_q8(_ptr(x), K, n_rows, ctypes.byref(out.c()), _stream(stream)))
+
+
+def gemv_q8(fmt: int, W, row_bytes: int, K: int, N: int, act: ActQ8, y, stream=None, accumulate=False) -> None:
+    """src/cuda/gemv.cuh:23-27."""
+    _check(lib().qwa_gemv_q8(fmt, _ptr(W), row_bytes, K, N, ctypes.byref(act.c()), _ptr(y), _stream(stream),
+                             1 if accumulate else 0))
+
+
+def gemv_q8n(fmt: int, W, row_bytes: int, K: int, N: int, act: ActQ8, nb: int, act_ld: int, y, y_ld: int,
+             stream=None, accumulate=False) -> None:
+    """src/cuda/gemv.cuh:33-36."""
+    _check(lib().qwa_gemv_q8n(fmt, _ptr(W), row_bytes, K, N, ctypes.byref(act.c()), nb, act_ld, _ptr(y), y_ld,
+                              _stream(stream), 1 if accumulate else 0))
+
+
+def gemv_bf16(W, K: int, N: int, x, y, stream=None) -> None:
+    """src/cuda/gemv.cuh:29-30."""
+    _check(lib().qwa_gemv_bf16(_ptr(W), K, N, _ptr(x), _ptr(y), _stream(stream)))
+
+
+def dequant_rows_f16(fmt: int, W, row_bytes: int, K: int, rows: int, out, stream=None) -> None:
+    """src/cuda/prefill.cuh:16-18."""
+    _check(lib().qwa_dequant_rows_f16(fmt, _ptr(W), row_bytes, K, rows, _ptr(out), _stream(stream)))

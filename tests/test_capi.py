@@ -123,6 +123,15 @@ int main() {
                hipStream_t) = deltanet_multi;
     void (*dr)(const DeltaNetParams&, const float*, const float*, const float*, const float*, int, int, float, void*,
                float*, __half*, hipStream_t) = deltanet_rows;
+    enum class QuantFormat : uint32_t { Q4_K = 12, IQ3_S = 21 };
+    if (!gemv_q8_supported(QuantFormat::Q4_K) || gemv_q8_supported(QuantFormat::IQ3_S)) return 5;
+    bool (*gq)(QuantFormat, const void*, size_t, int, int, const ActQ8&, float*, hipStream_t, bool) = gemv_q8;
+    bool (*gn)(QuantFormat, const void*, size_t, int, int, const ActQ8&, int, int, float*, int, hipStream_t, bool) =
+        gemv_q8n;
+    bool (*dq)(QuantFormat, const void*, size_t, int, int, __half*, hipStream_t) = dequant_rows_f16;
+    void (*qa)(const float*, int, int, ActQ8, hipStream_t) = quantize_act_q8;
+    void (*gb)(const uint16_t*, int, int, const float*, float*, hipStream_t) = gemv_bf16;
+    if (!gq || !gn || !dq || !qa || !gb) return 6;
     DNTokens tk;
     if (dn_work_bytes(1024) != (size_t)1024 * (10240 + 2 * 2048 + 2 * 48 + 16) * 4 || tk.qkv_split != (1 << 30)) return 4;
     return (fp && pp && ph && ds && dm && dr) ? 0 : 3;

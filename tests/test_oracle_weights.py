@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from wutil import random_rows
 
 F32 = np.float32
 
@@ -193,20 +194,6 @@ def np_dequant(fmt, W, K):
         dl = (d[:, None] * (ls - 32).astype(F32)).astype(F32)
         return (dl[:, :, None] * lev).astype(F32).reshape(-1)
     raise ValueError(fmt)
-
-
-def random_rows(fmt, N, K, seed):
-    """Random bytes with finite fp16 scales (random d / dmin fields rewritten as small normal values)."""
-    rng = np.random.default_rng(seed)
-    rb = O.w_row_bytes(fmt, K)
-    W = rng.integers(0, 256, (N, rb), dtype=np.uint8)
-    blocks = W.reshape(N, K // 256, rb // (K // 256))
-    offs = {O.W_Q4_K: [0, 2], O.W_Q2_K: [80, 82], O.W_Q6_K: [208], O.W_IQ4_XS: [0]}[fmt]
-    for o in offs:
-        vals = (rng.standard_normal(blocks.shape[:2]) * 0.01).astype(np.float16).view(np.uint16)
-        blocks[:, :, o] = (vals & 255).astype(np.uint8)
-        blocks[:, :, o + 1] = (vals >> 8).astype(np.uint8)
-    return W
 
 
 @pytest.mark.parametrize("fmt", [O.W_Q2_K, O.W_Q4_K, O.W_Q6_K, O.W_IQ4_XS], ids=["q2_k", "q4_k", "q6_k", "iq4_xs"])
