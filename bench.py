@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--positions", type=int, default=150000)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="headline decode only")
+    ap.add_argument("--consumer-only", action="store_true",
+                    help="print only the output-projection consumer figures (GEMV, fp16 GEMM)")
     ap.add_argument("--deltanet-only", action="store_true",
                     help="print only the Gated DeltaNet figures (for profiling those kernels)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -106,6 +108,9 @@ def main():
     torch.manual_seed(0)
     if args.deltanet_only:
         print(json.dumps({"deltanet": deltanet_extras(ops, torch, args.steps)}), flush=True)
+        return
+    if args.consumer_only:
+        print(json.dumps({"consumer": consumer_extras(ops, torch, args.steps)}), flush=True)
         return
     n, L = args.positions, args.layers
     kvt = ops.Q4_0
@@ -229,6 +234,7 @@ def main():
         extra["prefill_tflops"] = round(tflops, 1)
         extra["prefill_mfma_frac"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
         extra.update(deltanet_extras(ops, torch, args.steps))
+        extra.update(consumer_extras(ops, torch, args.steps))
         result["extra"] = extra
 
     if not args.no_cpu:
@@ -281,6 +287,48 @@ def deltanet_extras(ops, torch, steps, L=48):
     out["deltanet_prefill_tokens_per_s"] = round(B / (ms * 1e-3), 0)
     del layers
     torch.cuda.empty_cache()
+    return out
+
+
+def consumer_extras(ops, torch, steps):
+    """The attention output's consumers at the O-projection shape (6144 inputs, 5120 outputs): the decode GEMV over
+    one ActQ8 column (weights streamed once: bytes = the weight matrix) for two formats, as HIP-graph replays of 16
+    calls, and the prefill FP16 GEMM of a 1024-token chunk on hipBLASLt."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(HERE, "tests"))
+    K, N = 6144, 5120
+    out = {}
+    x = torch.randn((1, K), device="cuda")
+    a = ops.ActQ8.allocate(K)
+    ops.quantize_act_q8(x, K, 1, a)
+    y = torch.empty(N, device="cuda")
+    rng = np.random.default_rng(0)
+    for fmt, name in ((ops.W_Q4_K, "q4_k"), (ops.W_IQ4_XS, "iq4_xs")):
+        rb = ops.w_row_bytes(fmt, K)
+        Wn = rng.integers(0, 256, (N, rb), dtype=np.uint8)
+        blocks = Wn.reshape(N, K // 256, rb // (K // 256))
+        blocks[:, :, 1] = 0x1c  # every d (and Q4_K's dmin) field a small fp16 value: bytes xx 1c ~ 0.004
+        if fmt == ops.W_Q4_K:
+            blocks[:, :, 3] = 0x1c
+        W = [torch.from_numpy(Wn).cuda() for _ in range(4)]  # 4 copies: 71 MB, more than one XCD's caches
+
+        def run():
+            for i in range(16):
+                ops.gemv_q8(fmt, W[i % 4], rb, K, N, a, y)
+        ms = time_graph(torch, run, max(5, steps // 5))
+        us = ms * 1000.0 / 16
+        out[f"gemv_{name}_6144x5120_us"] = round(us, 3)
+        out[f"gemv_{name}_6144x5120_gbs"] = round(N * rb / (us * 1e-6) / 1e9, 1)
+        del W
+    B = 1024
+    g = ops.Gemm()
+    Wh = (torch.randn((N, K), device="cuda") * 0.05).half()
+    Xh = torch.randn((B, K), device="cuda").half()
+    Y = torch.empty((B, N), device="cuda")
+    ms = time_calls(torch, lambda: g.f16(Wh, N, K, Xh, K, B, Y, N), max(10, steps // 2), 3)
+    out["gemm_f16_1024x5120x6144_ms"] = round(ms, 4)
+    out["gemm_f16_tflops"] = round(2.0 * B * N * K / (ms * 1e-3) / 1e12, 1)
+    g.close()
     return out
 
 

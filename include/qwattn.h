@@ -236,6 +236,17 @@ int qwa_gemv_bf16(const uint16_t* W, int K, int N, const float* x, float* y, voi
  * reference dequantizer's fp32 value rounded to fp16 (nearest-even).  BF16 rows are accepted (row_bytes = 2 K). */
 int qwa_dequant_rows_f16(int fmt, const void* W, size_t row_bytes, int K, int rows, uint16_t* out, void* stream);
 
+/* FP16 GEMM of the prefill projections on hipBLASLt (replaces cublas_create / cublas_bind / cublas_destroy /
+ * gemm_f16, src/cuda/prefill.cuh:20-29): Y[b][n] (+)= sum_k X[b][k] W[n][k] for W [N][K] fp16, X [B][ldx] fp16,
+ * Y [B][ldy] fp32 (accumulate: beta = 1).  qwa_gemm_bind sets the default stream and a caller-owned workspace; after
+ * it no call allocates.  A NULL stream argument to qwa_gemm_f16 means the bound stream.  NULL from qwa_gemm_create
+ * means hipBLASLt could not be initialised. */
+void* qwa_gemm_create(void);
+int qwa_gemm_bind(void* handle, void* stream, void* workspace, size_t bytes);
+void qwa_gemm_destroy(void* handle);
+int qwa_gemm_f16(void* handle, const uint16_t* W, int N, int K, const uint16_t* X, int ldx, int B, float* Y, int ldy,
+                 int accumulate, void* stream);
+
 /* Opt-in kernel timing (no reference counterpart; the reference times phases with env-gated GPU timers,
  * src/runtime/engine.cpp:2477-2480): between qwa_profile_begin() and qwa_profile_end(), every launch of an
  * attention call's main kernel (decode: the split-K kernel; prefill: the MFMA kernel) is bracketed by two HIP events

@@ -17,7 +17,7 @@ LIB = os.path.join(OUT_DIR, "libqwattn.so")
 ARCH = "gfx950"
 
 SOURCES = ["capi.hip", "kv_append.hip", "attn_decode.hip", "attn_simple.hip", "attn_prefill.hip", "deltanet.hip",
-           "gemv.hip"]
+           "gemv.hip", "gemm.cpp"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -57,7 +57,8 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> str:
     with concurrent.futures.ThreadPoolExecutor(workers) as ex:
         objs = list(ex.map(lambda s: _compile(s, extra), SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-L/opt/rocm/lib", "-lhipblaslt",
+           "-Wl,-rpath,/opt/rocm/lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-4000:]}")

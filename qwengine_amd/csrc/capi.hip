@@ -331,6 +331,11 @@ int qwa_deltanet_rows(const qwa_dn_params* p, const float* qkv, const float* z, 
                     fn);
 }
 
+// status and message for the host-only sources of the library (gemm.cpp)
+extern "C" __attribute__((visibility("hidden"))) int qwa_fail_status(int status, const char* what) {
+    return fail(status, "%s", what);
+}
+
 // ---- consumers of the attention output (gemv.hip)
 size_t qwa_w_row_bytes(int fmt, long long K) { return qwa::w_row_bytes(fmt, K); }
 

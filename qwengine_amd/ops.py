@@ -99,6 +99,12 @@ EXPORTS = {
                                                  ctypes.c_void_p]),
     "qwa_dn_work_bytes": (ctypes.c_size_t, [ctypes.c_int]),
     "qwa_w_row_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_longlong]),
+    "qwa_gemm_create": (ctypes.c_void_p, []),
+    "qwa_gemm_bind": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+    "qwa_gemm_destroy": (None, [ctypes.c_void_p]),
+    "qwa_gemm_f16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                    ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p]),
     "qwa_gemv_q8_supported": (ctypes.c_int, [ctypes.c_int]),
     "qwa_quantize_act_q8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_ActQ8C),
                                            ctypes.c_void_p]),
@@ -480,3 +486,29 @@ def gemv_bf16(W, K: int, N: int, x, y, stream=None) -> None:
 def dequant_rows_f16(fmt: int, W, row_bytes: int, K: int, rows: int, out, stream=None) -> None:
     """src/cuda/prefill.cuh:16-18."""
     _check(lib().qwa_dequant_rows_f16(fmt, _ptr(W), row_bytes, K, rows, _ptr(out), _stream(stream)))
+
+
+class Gemm:
+    """hipBLASLt FP16 GEMM handle (mirror of cublas_create / cublas_bind / gemm_f16, src/cuda/prefill.cuh:20-29)."""
+
+    def __init__(self, workspace_bytes: int = 32 << 20, stream=None):
+        self.h = lib().qwa_gemm_create()
+        if not self.h:
+            raise QwaError("hipBLASLt could not be initialised")
+        self.ws = torch.empty(max(workspace_bytes, 1), dtype=torch.uint8, device="cuda")
+        _check(lib().qwa_gemm_bind(self.h, _stream(stream), _ptr(self.ws), workspace_bytes))
+
+    def f16(self, W, N: int, K: int, X, ldx: int, B: int, Y, ldy: int, accumulate=False, stream=None) -> None:
+        _check(lib().qwa_gemm_f16(self.h, _ptr(W), N, K, _ptr(X), ldx, B, _ptr(Y), ldy, 1 if accumulate else 0,
+                                  _stream(stream)))
+
+    def close(self) -> None:
+        if self.h:
+            lib().qwa_gemm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

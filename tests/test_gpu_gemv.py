@@ -134,3 +134,28 @@ def test_rejected_formats(gpu):
             ops.gemv_q8(fmt, W, 1024, 256, 4, a, y)
     with pytest.raises(ops.QwaError, match="row_bytes"):
         ops.gemv_q8(ops.W_Q4_K, W, 100, 256, 4, a, y)
+
+
+@pytest.mark.parametrize("N,K,B,ldx,ldy", [(5120, 6144, 1024, 6144, 5120), (37, 72, 5, 80, 40), (256, 512, 1, 512, 256)])
+def test_gemm_f16_vs_float64(gpu, N, K, B, ldx, ldy):
+    """Y = X W^T with fp16 inputs and fp32 accumulation (src/cuda/prefill.cuh:20-29) against float64 on the same fp16
+    values: within 1e-5 of sum |x| |w|; accumulate adds onto Y; columns past N in a padded Y row stay untouched."""
+    print(f"gemm_f16 N={N} K={K} B={B}", flush=True)
+    g = ops.Gemm()
+    W = (torch.randn((N, K), device="cuda") * 0.05).half()
+    X = torch.randn((B, ldx), device="cuda").half()
+    Y = torch.full((B, ldy), float("nan"), device="cuda")
+    g.f16(W, N, K, X, ldx, B, Y, ldy)
+    torch.cuda.synchronize()
+    Xd, Wd = X[:, :K].double(), W.double()
+    ref = Xd @ Wd.T
+    mag = Xd.abs() @ Wd.abs().T
+    assert ((Y[:, :N].double() - ref).abs() / mag).max().item() < 1e-5
+    if ldy > N:
+        assert torch.isnan(Y[:, N:]).all()
+    Y0 = Y.clone()
+    g.f16(W, N, K, X, ldx, B, Y, ldy, accumulate=True)
+    torch.cuda.synchronize()
+    assert ((Y[:, :N].double() - 2 * ref).abs() / mag).max().item() < 2e-5
+    assert torch.allclose(Y[:, :N], 2 * Y0[:, :N], rtol=1e-6, atol=1e-6)
+    g.close()
