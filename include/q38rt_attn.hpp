@@ -261,5 +261,18 @@ inline bool dequant_rows_f16(QF type, const void* W, size_t row_bytes, int K, in
     return true;
 }
 
+// src/cuda/prefill.cuh:20-29: the handle is this library's hipBLASLt context (the reference's cuBLAS handle)
+inline void* cublas_create() { return qwa_gemm_create(); }
+inline bool cublas_bind(void* h, hipStream_t st, void* workspace, size_t bytes) {
+    return qwa_gemm_bind(h, st, workspace, bytes) == QWA_OK;
+}
+inline void cublas_destroy(void* h) { qwa_gemm_destroy(h); }
+inline void gemm_f16(void* h, const __half* W, int N, int K, const __half* X, int ldx, int B, float* Y, int ldy,
+                     bool accumulate, hipStream_t st) {
+    detail::check(qwa_gemm_f16(h, reinterpret_cast<const uint16_t*>(W), N, K, reinterpret_cast<const uint16_t*>(X),
+                               ldx, B, Y, ldy, accumulate ? 1 : 0, st),
+                  "gemm_f16");
+}
+
 }  // namespace cuda
 }  // namespace q38rt

@@ -132,6 +132,10 @@ int main() {
     void (*qa)(const float*, int, int, ActQ8, hipStream_t) = quantize_act_q8;
     void (*gb)(const uint16_t*, int, int, const float*, float*, hipStream_t) = gemv_bf16;
     if (!gq || !gn || !dq || !qa || !gb) return 6;
+    void (*gm)(void*, const __half*, int, int, const __half*, int, int, float*, int, bool, hipStream_t) = gemm_f16;
+    void* (*cc)() = cublas_create;
+    bool (*cb)(void*, hipStream_t, void*, size_t) = cublas_bind;
+    if (!gm || !cc || !cb) return 7;
     DNTokens tk;
     if (dn_work_bytes(1024) != (size_t)1024 * (10240 + 2 * 2048 + 2 * 48 + 16) * 4 || tk.qkv_split != (1 << 30)) return 4;
     return (fp && pp && ph && ds && dm && dr) ? 0 : 3;
