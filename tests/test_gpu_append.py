@@ -138,3 +138,38 @@ def test_attn_prep_rows(gpu, oracle, kvt):
     ops.attn_prep_rows(qg, k, v, qn, kn, B, p0, rope, 1e-6, kvt, kv, q, gate)
     torch.cuda.synchronize()
     _check_prep(oracle, kvt, kv, p0, B, qg, k, v, qn, kn, q, gate, rope=rope)
+
+
+@pytest.mark.parametrize("kvt", [ops.Q8_0, ops.Q4_0], ids=lambda k: KV_NAMES[k])
+def test_attn_prep_multi_host_tails(gpu, kvt):
+    """RowSrc mapped-host tails (src/cuda/ops.cuh:24-34): row elements from `split` on come from pinned host rows of
+    stride host_ld.  Q / gate split mid-head, K split mid-row, V entirely on the host: q, gate and the stored K / V
+    bytes equal the all-device call's, and the device copies' NaN tails are never read."""
+    n, pos0, rope_pos0 = 5, 300, 4000
+    qg, k, v, qn, kn = _prep_inputs(n, 90 + kvt)
+
+    def run(src_qg, src_k, src_v):
+        kv = ops.KVLayer.allocate(kvt, 512)
+        q_out = torch.empty((n, 24, 256), device="cuda")
+        gate = torch.empty_like(q_out)
+        ops.attn_prep_multi(src_qg, src_k, src_v, qn, kn, pos0, rope_pos0, n, 1e7, 1e-6, kvt, kv, q_out, gate)
+        torch.cuda.synchronize()
+        return kv, q_out, gate
+
+    def split(t, width, at, pad):
+        dev = t.clone().reshape(n, width)
+        dev[:, at:] = float("nan")
+        host = torch.full((n, width - at + pad), float("nan"), pin_memory=True)
+        host[:, :width - at] = t.reshape(n, width)[:, at:].cpu()
+        return ops.RowSrc(dev, at, host, width - at + pad), host
+
+    kv0, q0, g0 = run(ops.RowSrc.device(qg, 12288), ops.RowSrc.device(k, 1024), ops.RowSrc.device(v, 1024))
+    sq, hq = split(qg, 12288, 5000, 3)
+    sk, hk = split(k, 1024, 300, 1)
+    sv, hv = split(v, 1024, 0, 0)
+    kv1, q1, g1 = run(sq, sk, sv)
+    assert torch.equal(q0, q1) and torch.equal(g0, g1)
+    assert torch.equal(kv0.k[:, pos0:pos0 + n], kv1.k[:, pos0:pos0 + n])
+    assert torch.equal(kv0.v[:, pos0:pos0 + n], kv1.v[:, pos0:pos0 + n])
+    assert torch.equal(kv0.ks[:, pos0:pos0 + n], kv1.ks[:, pos0:pos0 + n])
+    assert torch.equal(kv0.vs[:, pos0:pos0 + n], kv1.vs[:, pos0:pos0 + n])
