@@ -278,13 +278,21 @@ __global__ void __launch_bounds__(DN_HT) k_dn_head(qwa_dn_params p, int cin, qwa
 }
 
 // ------------------------------------------------------------------------------------------------------ prefill
+constexpr int DN_CT = 16;      // tokens per chunk of the chunked recurrence
+#ifndef QWA_DN_CW
+#define QWA_DN_CW 4
+#endif
+constexpr int DN_CW = QWA_DN_CW;        // waves per workgroup of the chunked recurrence (key dims split over them)
+constexpr int DN_TPW = 8 / DN_CW;       // 16-row key-dim tiles of the state per wave
+constexpr int DN_CP = 20;      // padded row (floats) of the transposed chunk tiles in LDS
+constexpr int DN_NCOEF = 704;  // per (chunk, head): T^T [16][20] | P^T [16][20] | gamma | E | c1 | c2
 struct DnRows {
     float* conv;   // [B][10240] after SiLU
     float* qn;     // [B][2048] L2-normalised q
     float* kn;     // [B][2048] L2-normalised k
     float* beta;   // [B][48]
     float* decay;  // [B][48]
-    float* kq;     // [B][16] qn . kn per key head
+    float* coef;   // [ceil(B / 16)][48][DN_NCOEF] per-chunk coefficients (k_dn_chunk_prep)
 };
 
 __host__ __device__ inline DnRows dn_rows_split(void* work, int B) {
@@ -300,11 +308,14 @@ __host__ __device__ inline DnRows dn_rows_split(void* work, int B) {
     f += (size_t)B * DN_VH;
     r.decay = f;
     f += (size_t)B * DN_VH;
-    r.kq = f;
+    r.coef = f;
     return r;
 }
 
-size_t dn_work_bytes(int B) { return (size_t)B * (DN_CH + 2 * DN_QK + 2 * DN_VH + DN_KH) * sizeof(float); }
+size_t dn_work_bytes(int B) {
+    return ((size_t)B * (DN_CH + 2 * DN_QK + 2 * DN_VH) + (size_t)((B + DN_CT - 1) / DN_CT) * DN_VH * DN_NCOEF) *
+           sizeof(float);
+}
 
 // out[t][c] = silu(sum_k w[c][k] in(t - 3 + k)), in(i) = qkv[i][c] for i >= 0, else row 3 + i of the old window
 __global__ void __launch_bounds__(256) k_dn_conv_rows(const float* __restrict__ qkv, const float* __restrict__ cs_old,
@@ -333,8 +344,7 @@ __global__ void __launch_bounds__(256) k_dn_conv_state(const float* __restrict__
     }
 }
 
-// per token: L2-normalised q and k of the 16 key heads and their dot product (wave w: key heads w, w + 4, ...),
-// beta and decay
+// per token: L2-normalised q and k of the 16 key heads (wave w: key heads w, w + 4, ...), beta and decay
 __global__ void __launch_bounds__(256) k_dn_prep_rows(DnRows r, const float* __restrict__ beta_raw,
                                                       const float* __restrict__ alpha_raw,
                                                       const float* __restrict__ dt_bias,
@@ -353,8 +363,6 @@ __global__ void __launch_bounds__(256) k_dn_prep_rows(DnRows r, const float* __r
         qd[lane + 64] = qb;
         kd[lane] = ka;
         kd[lane + 64] = kb;
-        const float kq = wave_sum(qa * ka + qb * kb);
-        if (lane == 0) r.kq[(size_t)t * DN_KH + kh] = kq;
     }
     if (threadIdx.x < DN_VH) {
         const int h = threadIdx.x;
@@ -365,111 +373,259 @@ __global__ void __launch_bounds__(256) k_dn_prep_rows(DnRows r, const float* __r
     }
 }
 
-// The recurrence over B tokens: grid (48 heads, 8 groups of 16 columns), 4 waves.  Lane (column jc = t / 16 of the
-// group, r16 = t % 16) holds the row quads r16 and r16 + 16 of its column for the whole call (each load / store
-// instruction covers 256 contiguous bytes per column).  Per token, with unit q, k and kq = q.k:
-//     sk = S^T k, sq = S^T q;  dk = (v - decay sk) beta;  o = decay sq + kq dk;  S = decay S + k dk^T
-// (the reference's S <- decay S; S += k ((v - S^T k) beta)^T; o = S^T q).  Blocks of DN_RT tokens are staged in LDS
-// double buffers; the next block's global loads are in flight while the current block computes.  core_out may alias
-// qkv: it is written only after the conv kernel has read qkv.
-constexpr int DN_RT = 16;                 // tokens per staged block
-constexpr int DN_RG = 8;                  // workgroups (column groups) per head
-constexpr int DN_RC = DN_HD / DN_RG;      // 16 columns per workgroup
-__global__ void __launch_bounds__(256) k_dn_recur_rows(DnRows r, float* __restrict__ state, int B,
+constexpr int DN_RG = 8;               // workgroups (column groups) per head of the chunked recurrence
+constexpr int DN_RC = DN_HD / DN_RG;   // 16 value columns per workgroup
+
+// ---- the chunked recurrence (prefill).  For a chunk of 16 tokens with S the state before it, decays g, write
+// strengths beta, G(s, t) = g_{s+1} ... g_t and gamma_t = g_0 ... g_t, the per-token rule
+//     S <- g S;  u = beta (v - S^T k);  S += k u^T;  o = S^T q
+// unrolls to
+//     a_t = S^T k_t, b_t = S^T q_t
+//     (I + L) U = W,  L[t][s] = beta_t G(s, t) k_s.k_t (s < t),  W_t = beta_t v_t - beta_t gamma_t a_t
+//     o_t = gamma_t b_t + sum_{s<=t} G(s, t) (k_s.q_t) u_s
+//     S'  = gamma_15 S + sum_s G(s, 15) k_s u_s^T.
+// The value dims are independent columns, so a workgroup owns 16 of them.  k_dn_chunk_prep computes, per (head,
+// chunk), T = (I + L)^-1, P = M' T with M'[t][s] = G(s, t) k_s.q_t, and the token scalars, so that U = T W and
+// O = gamma b + P W are independent; k_dn_chunk_rows keeps its 128 x 16 slice of
+// S in fp32 MFMA accumulators and applies a chunk as matrix products on v_mfma_f32_16x16x4_f32: K S and Q S (split over
+// the waves by key dims, summed through LDS), U = T W, O = gamma b + P W and the rank-16 state update.  Tokens past
+// B are padded with k = q = v = 0, beta = 0, g = 1, which change nothing.
+__device__ __forceinline__ f4 mfma4f32(float a, float b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__global__ void __launch_bounds__(256) k_dn_chunk_prep(DnRows r, int B) {
+    const int h = blockIdx.x, c = blockIdx.y, kh = h % DN_KH, t = threadIdx.x;
+    __shared__ float sk[DN_CT][DN_HD + 4], sq[DN_CT][DN_HD + 4];
+    __shared__ float sg[DN_CT], sb[DN_CT], sL[DN_CT][DN_CT + 1], sM[DN_CT][DN_CT + 1], sT[DN_CT][DN_CT + 1];
+    for (int e = t; e < DN_CT * (DN_HD / 4); e += 256) {
+        const int tok = e >> 5, f = e & 31, i = c * DN_CT + tok, ii = min(i, B - 1);
+        const float4 kv = *reinterpret_cast<const float4*>(r.kn + (size_t)ii * DN_QK + kh * DN_HD + 4 * f);
+        const float4 qv = *reinterpret_cast<const float4*>(r.qn + (size_t)ii * DN_QK + kh * DN_HD + 4 * f);
+        const bool in = i < B;
+        sk[tok][4 * f] = in ? kv.x : 0.0f; sk[tok][4 * f + 1] = in ? kv.y : 0.0f;
+        sk[tok][4 * f + 2] = in ? kv.z : 0.0f; sk[tok][4 * f + 3] = in ? kv.w : 0.0f;
+        sq[tok][4 * f] = in ? qv.x : 0.0f; sq[tok][4 * f + 1] = in ? qv.y : 0.0f;
+        sq[tok][4 * f + 2] = in ? qv.z : 0.0f; sq[tok][4 * f + 3] = in ? qv.w : 0.0f;
+    }
+    if (t < DN_CT) {
+        const int i = c * DN_CT + t, ii = min(i, B - 1);
+        const float gd = r.decay[(size_t)ii * DN_VH + h], bt = r.beta[(size_t)ii * DN_VH + h];
+        sg[t] = i < B ? gd : 1.0f;
+        sb[t] = i < B ? bt : 0.0f;
+    }
+    __syncthreads();
+    float* cf = r.coef + ((size_t)c * DN_VH + h) * DN_NCOEF;
+    {
+        // thread (s, u): the Gram entries k_s.k_u and k_s.q_u, L[u][s] and M'[u][s]
+        const int s = t >> 4, u = t & 15;
+        float kk0 = 0.0f, kk1 = 0.0f, kq0 = 0.0f, kq1 = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < DN_HD; i += 2) {
+            kk0 = fmaf(sk[s][i], sk[u][i], kk0);
+            kk1 = fmaf(sk[s][i + 1], sk[u][i + 1], kk1);
+            kq0 = fmaf(sk[s][i], sq[u][i], kq0);
+            kq1 = fmaf(sk[s][i + 1], sq[u][i + 1], kq1);
+        }
+        float G = 1.0f;
+        for (int e = s + 1; e <= u; e++) G *= sg[e];
+        sL[u][s] = s < u ? sb[u] * G * (kk0 + kk1) : 0.0f;
+        sM[u][s] = s <= u ? G * (kq0 + kq1) : 0.0f;
+    }
+    __syncthreads();
+    if (t < DN_CT) {
+        // column s = t of T = (I + L)^-1 by forward substitution: T[u][s] = [u == s] - sum_{r<u} L[u][r] T[r][s]
+        const int s = t;
+        float x[DN_CT];
+#pragma unroll
+        for (int u = 0; u < DN_CT; u++) {
+            float acc = u == s ? 1.0f : 0.0f;
+#pragma unroll
+            for (int q = 0; q < u; q++) acc = fmaf(-sL[u][q], x[q], acc);
+            x[u] = u < s ? 0.0f : acc;
+        }
+#pragma unroll
+        for (int u = 0; u < DN_CT; u++) {
+            cf[s * DN_CP + u] = x[u];  // T^T[s][u] = T[u][s]
+            sT[u][s] = x[u];
+        }
+        float gam = 1.0f, E = 1.0f;
+        for (int e = 0; e <= t; e++) gam *= sg[e];
+        for (int e = t + 1; e < DN_CT; e++) E *= sg[e];
+        cf[640 + t] = gam;
+        cf[656 + t] = E;
+        cf[672 + t] = sb[t];
+        cf[688 + t] = sb[t] * gam;
+    }
+    __syncthreads();
+    {
+        // P = M' T (so that O = gamma b + P W needs no U): P^T[s][u] = sum_{s<=x<=u} M'[u][x] T[x][s]
+        const int s = t >> 4, u = t & 15;
+        float acc = 0.0f;
+        for (int x = s; x <= u; x++) acc = fmaf(sM[u][x], sT[x][s], acc);
+        cf[320 + s * DN_CP + u] = acc;
+    }
+}
+
+// One chunk of k_dn_chunk_rows on its staged operands (see above).  st: this lane's 8 state values, updated.
+__device__ __forceinline__ void dn_chunk_step(float (*KT)[DN_CP], float (*QT)[DN_CP], float (*V)[DN_RC],
+                                              const float* C, float (*Red)[2][DN_CT][DN_CP], f4* st, int w, int l16,
+                                              int g4, int c, int B, int h, int grp, float oscale,
+                                              float* __restrict__ core_out) {
+    // 1) partial a = K S and b = Q S over this wave's key dims: A[t][i] = K[t][i], B[i][j] = S[i][j]
+    f4 pa = f4{0.0f, 0.0f, 0.0f, 0.0f}, pb = pa;
+#pragma unroll
+    for (int m = 0; m < DN_TPW; m++)
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            const int i = 16 * (DN_TPW * w + m) + 4 * g4 + rr;
+            pa = mfma4f32(KT[i][l16], st[m][rr], pa);
+            pb = mfma4f32(QT[i][l16], st[m][rr], pb);
+        }
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        Red[w][0][4 * g4 + rr][l16] = pa[rr];
+        Red[w][1][4 * g4 + rr][l16] = pb[rr];
+    }
+    __syncthreads();
+    float a[4], b[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        const int tt = 4 * g4 + rr;
+        float x = Red[0][0][tt][l16], y = Red[0][1][tt][l16];
+#pragma unroll
+        for (int v = 1; v < DN_CW; v++) {
+            x += Red[v][0][tt][l16];
+            y += Red[v][1][tt][l16];
+        }
+        a[rr] = x;
+        b[rr] = y;
+    }
+    // 2) U = T W and O = gamma b + P W with W[s][j] = c1_s v_s - c2_s a_s (this lane: s = 4 g4 + q; A operands
+    //    T[t][s] = T^T[s][t], P[t][s] = P^T[s][t] with t = l16)
+    f4 U = f4{0.0f, 0.0f, 0.0f, 0.0f}, O;
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) O[rr] = C[640 + 4 * g4 + rr] * b[rr];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int s = 4 * g4 + q;
+        const float Wv = fmaf(C[672 + s], V[s][l16], -C[688 + s] * a[q]);
+        U = mfma4f32(C[s * DN_CP + l16], Wv, U);
+        O = mfma4f32(C[320 + s * DN_CP + l16], Wv, O);
+    }
+    if (w == 0) {
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            const int tok = c * DN_CT + 4 * g4 + rr;
+            if (tok < B) core_out[(size_t)tok * DN_VD + h * DN_HD + grp * DN_RC + l16] = O[rr] * oscale;
+        }
+    }
+    // 4) S = gamma_15 S + K^T (E U): A[i][s] = K[s][i], B[s][j] = E_s U[s][j]
+    const float g15 = C[640 + DN_CT - 1];
+#pragma unroll
+    for (int m = 0; m < DN_TPW; m++) {
+        f4 acc = st[m] * g15;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int s = 4 * g4 + q;
+            acc = mfma4f32(KT[16 * (DN_TPW * w + m) + l16][s], C[656 + s] * U[q], acc);
+        }
+        st[m] = acc;
+    }
+}
+
+__global__ void __launch_bounds__(DN_CW * 64) __attribute__((amdgpu_waves_per_eu(DN_CW / 2, DN_CW / 2)))
+k_dn_chunk_rows(DnRows r, float* __restrict__ state, int B,
                                                        float* __restrict__ core_out) {
     const int h = blockIdx.x, grp = blockIdx.y, kh = h % DN_KH, t = threadIdx.x;
-    const int jc = t >> 4, r16 = t & 15, j = grp * DN_RC + jc;
-    __shared__ float4 sk[2][DN_RT][DN_HD / 4], sq[2][DN_RT][DN_HD / 4];
-    __shared__ float4 sc[2][DN_RT];  // decay, beta, kq
-    __shared__ float sv[2][DN_RT][DN_RC], so[DN_RT][DN_RC];
-    float4* Sq = reinterpret_cast<float4*>(state + (size_t)h * DN_HD * DN_HD + (size_t)j * DN_HD) + r16;
-    const float4 s0 = Sq[0], s1 = Sq[16];
-    float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    const float oscale = 1.0f / sqrtf((float)DN_HD);
-
-    // staging: thread (token tt = t / 16, f = t % 16) moves float4 f and f + 16 of q and k, v column f, and (t < 16)
-    // the scalars of token t; slots past B read token 0 and are not used
-    const int st_tt = t >> 4, st_f = t & 15;
-    float4 pk0, pk1, pq0, pq1, pc;
-    float pv;
-    auto fetch = [&](int b0) {
-        const int i = min(b0 + st_tt, B - 1);
-        const float4* kr = reinterpret_cast<const float4*>(r.kn + (size_t)i * DN_QK + kh * DN_HD);
-        const float4* qr = reinterpret_cast<const float4*>(r.qn + (size_t)i * DN_QK + kh * DN_HD);
-        pk0 = kr[st_f];
-        pk1 = kr[st_f + 16];
-        pq0 = qr[st_f];
-        pq1 = qr[st_f + 16];
-        pv = r.conv[(size_t)i * DN_CH + 2 * DN_QK + h * DN_HD + grp * DN_RC + st_f];
-        const int ic = min(b0 + t, B - 1);
-        if (t < DN_RT)
-            pc = make_float4(r.decay[(size_t)ic * DN_VH + h], r.beta[(size_t)ic * DN_VH + h],
-                             r.kq[(size_t)ic * DN_KH + kh], 0.0f);
-    };
-    auto stage = [&](int buf) {
-        sk[buf][st_tt][st_f] = pk0;
-        sk[buf][st_tt][st_f + 16] = pk1;
-        sq[buf][st_tt][st_f] = pq0;
-        sq[buf][st_tt][st_f + 16] = pq1;
-        sv[buf][st_tt][st_f] = pv;
-        if (t < DN_RT) sc[buf][t] = pc;
-    };
-    fetch(0);
-    stage(0);
-    __syncthreads();
-    for (int b0 = 0, buf = 0; b0 < B; b0 += DN_RT, buf ^= 1) {
-        const int nt = min(DN_RT, B - b0);
-        if (b0 + DN_RT < B) fetch(b0 + DN_RT);
-        // two operand sets alternate so that the next token's LDS reads overlap the current token's arithmetic
-        struct Op {
-            float4 ka, kb, qa, qb, c;
-            float v;
-        };
-        auto load = [&](Op& op, int tt) {
-            op.ka = sk[buf][tt][r16];
-            op.kb = sk[buf][tt][r16 + 16];
-            op.qa = sq[buf][tt][r16];
-            op.qb = sq[buf][tt][r16 + 16];
-            op.c = sc[buf][tt];
-            op.v = sv[buf][tt][jc];
-        };
-        auto apply = [&](const Op& op, int tt) {
-            const float kr[8] = {op.ka.x, op.ka.y, op.ka.z, op.ka.w, op.kb.x, op.kb.y, op.kb.z, op.kb.w};
-            const float qr[8] = {op.qa.x, op.qa.y, op.qa.z, op.qa.w, op.qb.x, op.qb.y, op.qb.z, op.qb.w};
-            float k0 = 0.0f, k1 = 0.0f, q0 = 0.0f, q1 = 0.0f;
+    const int w = t >> 6, l = t & 63, g4 = l >> 4, l16 = l & 15;
+    __shared__ __attribute__((aligned(16))) float sKT[2][DN_HD][DN_CP], sQT[2][DN_HD][DN_CP];
+    __shared__ float sV[2][DN_CT][DN_RC];
+    __shared__ __attribute__((aligned(16))) float sC[2][DN_NCOEF];
+    // the waves' partial K S / Q S; one buffer: the next chunk writes it only after the barrier that ends this one
+    __shared__ float sRed[DN_CW][2][DN_CT][DN_CP];
+    // this lane's state: key-dim tiles m = DN_TPW w .. DN_TPW w + DN_TPW - 1, S[16 m + 4 g4 + rr][grp * 16 + l16]
+    const int j = grp * DN_RC + l16;
+    float* Sj = state + (size_t)h * DN_HD * DN_HD + (size_t)j * DN_HD;
+    f4 st[DN_TPW];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                k0 = fmaf(s[2 * e], kr[2 * e], k0);
-                k1 = fmaf(s[2 * e + 1], kr[2 * e + 1], k1);
-                q0 = fmaf(s[2 * e], qr[2 * e], q0);
-                q1 = fmaf(s[2 * e + 1], qr[2 * e + 1], q1);
-            }
-            const float skv = row16_sum(k0 + k1), sqv = row16_sum(q0 + q1);
-            const float dk = fmaf(-op.c.x, skv, op.v) * op.c.y;
-            const float oj = fmaf(op.c.x, sqv, op.c.z * dk);
-#pragma unroll
-            for (int e = 0; e < 8; e++) s[e] = fmaf(kr[e], dk, s[e] * op.c.x);
-            if (r16 == 0) so[tt][jc] = oj * oscale;
-        };
-        Op opa, opb;
-        load(opa, 0);
-        for (int tt = 0; tt < nt; tt += 2) {
-            if (tt + 1 < nt) load(opb, tt + 1);
-            apply(opa, tt);
-            if (tt + 1 >= nt) break;
-            if (tt + 2 < nt) load(opa, tt + 2);
-            apply(opb, tt + 1);
-        }
-        __syncthreads();  // outputs complete; every read of buffer buf done
-        {
-            const int tt = t >> 4, e = t & 15;
-            if (tt < nt) core_out[(size_t)(b0 + tt) * DN_VD + h * DN_HD + grp * DN_RC + e] = so[tt][e];
-        }
-        if (b0 + DN_RT < B) stage(buf ^ 1);
-        __syncthreads();
+    for (int m = 0; m < DN_TPW; m++) {
+        const float4 v = *reinterpret_cast<const float4*>(Sj + 16 * (DN_TPW * w + m) + 4 * g4);
+        st[m] = f4{v.x, v.y, v.z, v.w};
     }
-    Sq[0] = make_float4(s[0], s[1], s[2], s[3]);
-    Sq[16] = make_float4(s[4], s[5], s[6], s[7]);
+    const float oscale = 1.0f / sqrtf((float)DN_HD);
+    const int nch = (B + DN_CT - 1) / DN_CT;
+    // staging: thread (token t % 16, f = t / 16) moves k / q dims DN_SD f .. DN_SD f + DN_SD - 1 (transposed; tokens
+    // past B as zero), thread t < 256 (token t / 16, column t % 16) one v, threads < 176 one float4 of the coefficients.  Two register sets
+    // hold chunks c + 1 and c + 2 (set A odd chunks, set B even ones), so a chunk's loads have two chunks of compute
+    // to arrive.
+    constexpr int DN_SD = DN_HD * DN_CT / (64 * DN_CW);  // k / q dims staged per thread
+    constexpr int DN_SNF = DN_SD / 4;
+    const int s_tok = t & 15, s_f = t >> 4, v_tok = (t >> 4) & 15, v_col = t & 15;
+#define DN_CDECL(X)                                                                                               \
+    float4 X##k[DN_SNF], X##q[DN_SNF], X##c;                                                                     \
+    float X##v;                                                                                                   \
+    bool X##in, X##vin
+#define DN_CFETCH(X, C)                                                                                           \
+    do {                                                                                                          \
+        const int i_ = (C) * DN_CT + s_tok, ii_ = min(i_, B - 1);                                                \
+        X##in = i_ < B;                                                                                           \
+        const float4* kr_ = reinterpret_cast<const float4*>(r.kn + (size_t)ii_ * DN_QK + kh * DN_HD + DN_SD * s_f); \
+        const float4* qr_ = reinterpret_cast<const float4*>(r.qn + (size_t)ii_ * DN_QK + kh * DN_HD + DN_SD * s_f); \
+        _Pragma("unroll") for (int e_ = 0; e_ < DN_SNF; e_++) {                                                   \
+            X##k[e_] = kr_[e_];                                                                                   \
+            X##q[e_] = qr_[e_];                                                                                   \
+        }                                                                                                         \
+        const int iv_ = (C) * DN_CT + v_tok;                                                                      \
+        X##vin = iv_ < B && t < DN_CT * DN_RC;                                                                    \
+        X##v = r.conv[(size_t)min(iv_, B - 1) * DN_CH + 2 * DN_QK + h * DN_HD + grp * DN_RC + v_col];            \
+        if (t < DN_NCOEF / 4)                                                                                     \
+            X##c = *reinterpret_cast<const float4*>(r.coef + ((size_t)(C) * DN_VH + h) * DN_NCOEF + 4 * t);      \
+    } while (0)
+#define DN_CSTAGE(X, BUF)                                                                                         \
+    do {                                                                                                          \
+        _Pragma("unroll") for (int e_ = 0; e_ < DN_SNF; e_++) {                                                   \
+            const float kx_[4] = {X##k[e_].x, X##k[e_].y, X##k[e_].z, X##k[e_].w};                                \
+            const float qx_[4] = {X##q[e_].x, X##q[e_].y, X##q[e_].z, X##q[e_].w};                                \
+            _Pragma("unroll") for (int d_ = 0; d_ < 4; d_++) {                                                    \
+                sKT[BUF][DN_SD * s_f + 4 * e_ + d_][s_tok] = X##in ? kx_[d_] : 0.0f;                              \
+                sQT[BUF][DN_SD * s_f + 4 * e_ + d_][s_tok] = X##in ? qx_[d_] : 0.0f;                              \
+            }                                                                                                     \
+        }                                                                                                         \
+        if (t < DN_CT * DN_RC) sV[BUF][v_tok][v_col] = X##vin ? X##v : 0.0f;                                      \
+        if (t < DN_NCOEF / 4) *reinterpret_cast<float4*>(&sC[BUF][4 * t]) = X##c;                                 \
+    } while (0)
+    DN_CDECL(ra_);
+    DN_CDECL(rb_);
+    DN_CFETCH(ra_, 0);
+    DN_CSTAGE(ra_, 0);
+    if (1 < nch) DN_CFETCH(ra_, 1);
+    if (2 < nch) DN_CFETCH(rb_, 2);
+    __syncthreads();
+    // one chunk on LDS buffer BUF; then chunk C + 1 (register set X) is staged into the other buffer and chunk C + 3
+    // fetched into X
+#define DN_CHUNK(C, BUF, X)                                                                                       \
+    do {                                                                                                          \
+        dn_chunk_step(sKT[BUF], sQT[BUF], sV[BUF], sC[BUF], sRed, st, w, l16, g4, (C), B, h, grp, oscale,       \
+                      core_out);                                                                                  \
+        if ((C) + 1 < nch) {                                                                                      \
+            DN_CSTAGE(X, (BUF) ^ 1);                                                                              \
+            if ((C) + 3 < nch) DN_CFETCH(X, (C) + 3);                                          \
+        }                                                                                                         \
+        __syncthreads();                                                                                          \
+    } while (0)
+    for (int c = 0; c < nch; c += 2) {
+        DN_CHUNK(c, 0, ra_);
+        if (c + 1 < nch) DN_CHUNK(c + 1, 1, rb_);
+    }
+#undef DN_CHUNK
+#undef DN_CDECL
+#undef DN_CFETCH
+#undef DN_CSTAGE
+#pragma unroll
+    for (int m = 0; m < DN_TPW; m++)
+        *reinterpret_cast<float4*>(Sj + 16 * (DN_TPW * w + m) + 4 * g4) =
+            make_float4(st[m][0], st[m][1], st[m][2], st[m][3]);
 }
 
 // gated RMSNorm per (token, value head), fp16 out: grid (B, 48), 128 threads
@@ -505,7 +661,9 @@ hipError_t launch_dn_rows(const qwa_dn_params& p, const float* qkv, const float*
     hipLaunchKernelGGL(k_dn_conv_rows, dim3(DN_CH / 256, B), dim3(256), 0, st, qkv, cs_old, p.conv_w, r.conv);
     hipLaunchKernelGGL(k_dn_conv_state, dim3(DN_CH / 256), dim3(256), 0, st, qkv, cs_old, B, cs_new);
     hipLaunchKernelGGL(k_dn_prep_rows, dim3(B), dim3(256), 0, st, r, beta_raw, alpha_raw, p.dt_bias, p.ssm_a, eps);
-    hipLaunchKernelGGL(k_dn_recur_rows, dim3(DN_VH, DN_RG), dim3(256), 0, st, r, p.ssm_state, B, core_out);
+    const int nch = (B + DN_CT - 1) / DN_CT;
+    hipLaunchKernelGGL(k_dn_chunk_prep, dim3(DN_VH, nch), dim3(256), 0, st, r, B);
+    hipLaunchKernelGGL(k_dn_chunk_rows, dim3(DN_VH, DN_RG), dim3(DN_CW * 64), 0, st, r, p.ssm_state, B, core_out);
     hipLaunchKernelGGL(k_dn_gnorm_rows, dim3(B, DN_VH), dim3(128), 0, st, core_out, z, p.ssm_norm, eps, o16);
     return hipGetLastError();
 }

@@ -137,7 +137,7 @@ int main() {
     bool (*cb)(void*, hipStream_t, void*, size_t) = cublas_bind;
     if (!gm || !cc || !cb) return 7;
     DNTokens tk;
-    if (dn_work_bytes(1024) != (size_t)1024 * (10240 + 2 * 2048 + 2 * 48 + 16) * 4 || tk.qkv_split != (1 << 30)) return 4;
+    if (dn_work_bytes(1024) != ((size_t)1024 * (10240 + 2 * 2048 + 2 * 48) + 64 * 48 * 704) * 4 || tk.qkv_split != (1 << 30)) return 4;
     return (fp && pp && ph && ds && dm && dr) ? 0 : 3;
 }
 '''
