@@ -7,10 +7,11 @@
 //    issues while the other's MFMAs run; a wave owns 32 (query, head) rows (two 16-row MFMA tiles), so every K / V
 //    fragment read from LDS feeds two MFMAs; a workgroup owns 256 consecutive rows of one KV head
 //    (row r = 6 * token + head);
-//  * keys are walked in 32-key tiles.  The raw quantized bytes of a tile go HBM -> LDS by direct-to-LDS loads
-//    (no registers) two tiles ahead; all threads then dequantise the next tile cooperatively into fp16 LDS tiles, K as
-//    [key][dim] and V transposed as [dim][key], so both MFMA A-operands are single 16-byte LDS reads; one barrier per
-//    tile;
+//  * keys are walked in 32-key tiles.  k_pf_image first dequantises every tile of the call's KV range once into an
+//    fp16 image (K as [key][dim], V transposed as [dim][key], XOR-swizzled 16-byte units), so both MFMA A-operands
+//    are single conflict-free 16-byte LDS reads; k_prefill copies the images HBM -> LDS by direct-to-LDS loads (no
+//    registers) two tiles ahead, one barrier per tile.  Built with QWA_PF_IMAGE=0, the raw quantized bytes go to
+//    LDS instead and all threads dequantise the next tile cooperatively inside the loop;
 //  * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16 (fp32 accumulation); P^T comes out of the S^T
 //    accumulator already in B-operand layout; online softmax in fp32 with a lazy rescale;
 //  * the causal key range of a row block is cut into PF_NS fixed splits (one workgroup each) so that the
@@ -18,6 +19,8 @@
 //    a library-owned device buffer and k_pf_combine merges the splits in a fixed order, normalises, applies the
 //    sigmoid gate and writes fp16.  Chunks longer than PF_MAXB tokens run as several passes.
 #include <float.h>
+
+#include <mutex>
 
 #include "kv_operands.hpp"
 #include "launch.hpp"
@@ -122,6 +125,12 @@ __device__ __forceinline__ void wait_vm(int n) {
         case 4: wait_vmcnt<4>(); break;
         case 5: wait_vmcnt<5>(); break;
         case 6: wait_vmcnt<6>(); break;
+        case 7: wait_vmcnt<7>(); break;
+        case 8: wait_vmcnt<8>(); break;
+        case 9: wait_vmcnt<9>(); break;
+        case 10: wait_vmcnt<10>(); break;
+        case 11: wait_vmcnt<11>(); break;
+        case 12: wait_vmcnt<12>(); break;
         default: wait_vmcnt<0>(); break;
     }
 }
@@ -223,6 +232,60 @@ __device__ __forceinline__ void pf_convert(const uint8_t* raw, _Float16* Ks, _Fl
     }
 }
 
+#ifndef QWA_PF_IMAGE
+#define QWA_PF_IMAGE 1
+#endif
+// fp16 tile images: the KV range is dequantised once per call (k_pf_image), not once per row block inside the loop
+constexpr bool PF_IMAGE = QWA_PF_IMAGE != 0;
+constexpr int PF_IMG_K = PF_TILE * HD * 2;      // bytes of the K part of an image: [32 keys][256 dims] fp16
+constexpr int PF_IMG_BYTES = 2 * PF_IMG_K;      // K part, then V^T part [256 dims][32 keys] fp16
+constexpr int PF_IMG_NBUF = 3;   // images in LDS: the one computed on and two in flight
+constexpr int PF_IMG_AHEAD = 2;
+
+// Image layout (unpadded, so that a direct-to-LDS copy of 1 KB per instruction reproduces it in LDS, and XOR-swizzled
+// in 16-byte units so that the MFMA operand reads stay conflict-free without padding):
+//  * K: key r, 16-byte unit c (dims 8c .. 8c + 7, in the permuted order of pf_convert_kv) at byte 512 r + 16 (c ^ (r & 7));
+//  * V^T: dim d, unit c (keys 8c .. 8c + 7 in P^T operand order) at byte PF_IMG_K + 64 d + 16 (c ^ ((d >> 1) & 3)).
+__device__ __forceinline__ int pf_img_k_off(int r, int c) { return 512 * r + 16 * (c ^ (r & 7)); }
+__device__ __forceinline__ int pf_img_v_off(int d, int c) { return PF_IMG_K + 64 * d + 16 * (c ^ ((d >> 1) & 3)); }
+
+// One 32-key tile of one KV head per workgroup (grid (tiles, NKV), PF_THREADS threads): the same direct-to-LDS load
+// and the same conversion as the in-loop path (so the fp16 values are identical), then a swizzled copy to the image.
+// Keys past kmax re-read key kmax, as in the loop.
+template <int KVT>
+__global__ void __launch_bounds__(PF_THREADS) k_pf_image(qwa_kv_layer kv, int kmax, int ntiles, uint8_t* __restrict__ img) {
+    using L = PfRaw<KVT>;
+    __shared__ __attribute__((aligned(16))) uint8_t s_raw[L::BYTES];
+    __shared__ __attribute__((aligned(16))) _Float16 s_k[PF_TILE * KS_LD];
+    __shared__ __attribute__((aligned(16))) _Float16 s_vt[HD * VT_LD];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(t >> 6));
+    const int tile = blockIdx.x, g = blockIdx.y;
+    pf_issue<KVT>(lds_addr(s_raw), kv, (size_t)g * kv.capacity, tile * PF_TILE, kmax, wave, lane);
+    wait_vmcnt<0>();
+    __syncthreads();
+    pf_convert<KVT>(s_raw, s_k, s_vt, t);
+    __syncthreads();
+    uint8_t* dst = img + ((size_t)g * ntiles + tile) * PF_IMG_BYTES;
+    for (int u = t; u < PF_IMG_K / 16; u += PF_THREADS) {
+        const int r = u >> 5, c = u & 31;
+        *reinterpret_cast<uint4*>(dst + pf_img_k_off(r, c)) = *reinterpret_cast<const uint4*>(s_k + r * KS_LD + 8 * c);
+    }
+    for (int u = t; u < PF_IMG_K / 16; u += PF_THREADS) {
+        const int d = u >> 2, c = u & 3;
+        *reinterpret_cast<uint4*>(dst + pf_img_v_off(d, c)) = *reinterpret_cast<const uint4*>(s_vt + d * VT_LD + 8 * c);
+    }
+}
+
+// this wave's share of the direct-to-LDS copy of one image: 1 KB instructions wave, wave + 8, ...
+__device__ __forceinline__ void pf_issue_img(uint32_t lds, const uint8_t* src, int wave, int lane) {
+#pragma unroll
+    for (int c = 0; c < PF_IMG_BYTES / 1024 / PF_WAVES; c++) {
+        const int i = wave + PF_WAVES * c;
+        dma_sv<16>(lds + 1024 * i, src, (uint32_t)(1024 * i + 16 * lane));
+    }
+}
+
 __device__ __forceinline__ h8 lds_h8(const _Float16* p) { return *reinterpret_cast<const h8*>(p); }
 
 // max of three floats in one instruction (fmaxf would first canonicalize each MFMA result; scores are never sNaN)
@@ -251,14 +314,19 @@ __device__ __forceinline__ float rows_sum(float x) {
 
 // One split of one row block: grid (row blocks, NKV, PF_NS).  Tokens 0 .. B-1 of this pass sit at cache positions
 // p0 .. p0 + B - 1.
-template <int KVT>
+// IMG: tiles come as fp16 images (k_pf_image) of img_tiles tiles per KV head, copied straight into LDS; otherwise as
+// raw quantized bytes dequantised in the loop.
+template <int KVT, bool IMG>
 __global__ void __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(PF_WPE, PF_WPE)))
-k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, unsigned long long* prof) {
+k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uint8_t* __restrict__ img, int img_tiles,
+          unsigned long long* prof) {
     prof_start(prof);
     using L = PfRaw<KVT>;
-    __shared__ __attribute__((aligned(16))) uint8_t s_raw[L::NBUF][L::BYTES];
-    __shared__ __attribute__((aligned(16))) _Float16 s_k[2][PF_TILE * KS_LD];
-    __shared__ __attribute__((aligned(16))) _Float16 s_vt[2][HD * VT_LD];
+    constexpr int NBUF = IMG ? PF_IMG_NBUF : L::NBUF;
+    constexpr int AHEAD = IMG ? PF_IMG_AHEAD : NBUF - 1;
+    __shared__ __attribute__((aligned(16))) uint8_t s_raw[NBUF][IMG ? PF_IMG_BYTES : L::BYTES];
+    __shared__ __attribute__((aligned(16))) _Float16 s_k[IMG ? 1 : 2][IMG ? 8 : PF_TILE * KS_LD];
+    __shared__ __attribute__((aligned(16))) _Float16 s_vt[IMG ? 1 : 2][IMG ? 8 : HD * VT_LD];
     const int t = threadIdx.x, lane = t & 63, i16 = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane((int)(t >> 6));
     const int g = blockIdx.y, sp = blockIdx.z;
@@ -270,10 +338,11 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, unsigned 
     const int n_tiles = kmax / PF_TILE + 1;
     const int tb = sp * n_tiles / PF_NS, nt = (sp + 1) * n_tiles / PF_NS - tb;
     const size_t rowbase = (size_t)g * kv.capacity;
-    const int nvm = L::count(wave);
-    uint32_t raw_lds[L::NBUF];
+    const int nvm = IMG ? PF_IMG_BYTES / 1024 / PF_WAVES : L::count(wave);
+    uint32_t raw_lds[NBUF];
 #pragma unroll
-    for (int b = 0; b < L::NBUF; b++) raw_lds[b] = lds_addr(s_raw[b]);
+    for (int b = 0; b < NBUF; b++) raw_lds[b] = lds_addr(s_raw[b]);
+    const uint8_t* isrc = IMG ? img + (size_t)g * img_tiles * PF_IMG_BYTES : nullptr;
 
     // this lane's rows (token r / 6, head r % 6) and last visible key qpos; Q / 16 as the fp16 B operand
     int qpos[PF_RT];
@@ -310,7 +379,15 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, unsigned 
         for (int dt = 0; dt < 16; dt++) o[rt][dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    if (nt > 0) {
+    if (IMG && nt > 0) {
+        // prologue: images 0 .. AHEAD - 1 in flight, image 0 landed
+        wait_vmcnt<0>();  // the Q loads; from here on vmcnt counts only the tile loads
+#pragma unroll
+        for (int i = 0; i < AHEAD; i++)
+            pf_issue_img(raw_lds[i], isrc + (size_t)(tb + min(i, nt - 1)) * PF_IMG_BYTES, wave, lane);
+        wait_vm(nvm * (AHEAD - 1));
+        __syncthreads();
+    } else if (nt > 0) {
         // prologue: raw tiles 0 .. AHEAD - 1 in flight, tile 0 dequantised (and, with AHEAD >= 2, tile 1 landed)
         wait_vmcnt<0>();  // the Q loads; from here on vmcnt counts only the tile loads
 #pragma unroll
@@ -327,23 +404,44 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, unsigned 
     // LDS work (dequantisation, softmax) while the other's MFMAs run:
     //   waves 0-3: convert | S       | softmax | PV
     //   waves 4-7: S       | softmax | PV      | convert
+    // With images there is no conversion and every wave runs S | softmax | PV.
     const bool lead = (wave & PF_GROUP_BIT) == 0;
+    h8 pb[PF_RT];
+    auto pv = [&](const _Float16* Vt) {
+        h8 vf[PF_VD];
+        const _Float16* vrow = IMG ? Vt + i16 * PF_TILE + 8 * (lg ^ ((i16 >> 1) & 3)) : Vt + i16 * VT_LD + 8 * lg;
+        constexpr int vstep = IMG ? 16 * PF_TILE : 16 * VT_LD;
+#pragma unroll
+        for (int dt = 0; dt < PF_VD - 1; dt++) vf[dt] = lds_h8(vrow + vstep * dt);
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) {
+            if (dt + PF_VD - 1 < 16) vf[(dt + PF_VD - 1) % PF_VD] = lds_h8(vrow + vstep * (dt + PF_VD - 1));
+#pragma unroll
+            for (int rt = 0; rt < PF_RT; rt++) o[rt][dt] = mfma16(vf[dt % PF_VD], pb[rt], o[rt][dt]);
+        }
+    };
     for (int i = 0; i < nt; i++) {
         const int k0 = (tb + i) * PF_TILE, cur = i & 1;
         // tile i + AHEAD (the last tile again near the end: a harmless re-read) into the raw buffer freed last
         // iteration
-        pf_issue<KVT>(raw_lds[(i + L::AHEAD) % L::NBUF], kv, rowbase, (tb + min(i + L::AHEAD, nt - 1)) * PF_TILE,
-                      kmax, wave, lane);
-        const _Float16* Ks = s_k[cur];
-        const _Float16* Vt = s_vt[cur];
+        if constexpr (IMG)
+            pf_issue_img(raw_lds[(i + AHEAD) % NBUF], isrc + (size_t)(tb + min(i + AHEAD, nt - 1)) * PF_IMG_BYTES,
+                         wave, lane);
+        else
+            pf_issue<KVT>(raw_lds[(i + AHEAD) % NBUF], kv, rowbase, (tb + min(i + AHEAD, nt - 1)) * PF_TILE, kmax,
+                          wave, lane);
+        const _Float16* Ks = IMG ? reinterpret_cast<const _Float16*>(s_raw[i % NBUF]) : s_k[cur];
+        const _Float16* Vt = IMG ? Ks + PF_IMG_K / 2 : s_vt[cur];
 
         // the next tile's raw bytes landed before the last barrier: dequantise them into the other fp16 tile
         auto convert = [&]() {
-            if constexpr (L::AHEAD >= 2) pf_convert<KVT>(s_raw[(i + 1) % L::NBUF], s_k[cur ^ 1], s_vt[cur ^ 1], t);
+            if constexpr (!IMG && AHEAD >= 2) pf_convert<KVT>(s_raw[(i + 1) % NBUF], s_k[cur ^ 1], s_vt[cur ^ 1], t);
         };
 
         f4 sc[PF_RT][PF_KT];
-        h8 pb[PF_RT];
+        // image K operand bases: row i16, unit lg ^ (i16 & 3), s shifted by +-1 when bit 2 of i16 is set
+        const _Float16* kimg_e = Ks + i16 * HD + 8 * (lg ^ (i16 & 3)) + 32 * ((i16 >> 2) & 1);
+        const _Float16* kimg_o = kimg_e - 64 * ((i16 >> 2) & 1);
         // ---- S^T = K Q^T for PF_KT key tiles of 16 (lane: key k0 + 16 k4 + 4 lg + i, row (rt, i16))
         auto scores = [&]() {
 #pragma unroll
@@ -354,7 +452,9 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, unsigned 
             for (int s = 0; s < 8; s++) {
 #pragma unroll
                 for (int k4 = 0; k4 < PF_KT; k4++) {
-                    const h8 a = lds_h8(Ks + (16 * k4 + i16) * KS_LD + 8 * lg + 32 * s);
+                    // swizzled unit (4 s + lg) ^ x = 4 (s ^ (x >> 2)) + (lg ^ (x & 3)): two lane bases, even / odd s
+                    const h8 a = IMG ? lds_h8((s & 1 ? kimg_o : kimg_e) + (16 * k4) * HD + 32 * s)
+                                     : lds_h8(Ks + (16 * k4 + i16) * KS_LD + 8 * lg + 32 * s);
 #pragma unroll
                     for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = mfma16(a, qb[rt][s], sc[rt][k4]);
                 }
@@ -406,29 +506,19 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, unsigned 
             }
         };
 
-        // ---- O^T += V^T P^T over 16 dim tiles; the fragment of dim tile dt + PF_VD - 1 is read while dt multiplies
-        auto pv = [&]() {
-            h8 vf[PF_VD];
-#pragma unroll
-            for (int dt = 0; dt < PF_VD - 1; dt++) vf[dt] = lds_h8(Vt + (16 * dt + i16) * VT_LD + 8 * lg);
-#pragma unroll
-            for (int dt = 0; dt < 16; dt++) {
-                if (dt + PF_VD - 1 < 16)
-                    vf[(dt + PF_VD - 1) % PF_VD] = lds_h8(Vt + (16 * (dt + PF_VD - 1) + i16) * VT_LD + 8 * lg);
-#pragma unroll
-                for (int rt = 0; rt < PF_RT; rt++) o[rt][dt] = mfma16(vf[dt % PF_VD], pb[rt], o[rt][dt]);
-            }
-        };
-
-        if (lead) convert();
+        if (!IMG && lead) convert();
         scores();
         softmax();
-        pv();
-        if (!lead) convert();
+        pv(Vt);
+        if (!IMG && !lead) convert();
 
-        if constexpr (L::AHEAD >= 2) {
+        if constexpr (IMG) {
+            // image i + 1 must have landed before the next iteration reads it; image i + 2 may stay in flight
+            wait_vm(nvm * (AHEAD - 1));
+            __syncthreads();
+        } else if constexpr (AHEAD >= 2) {
             // tile i + 2 must have landed before the next iteration dequantises it; later tiles may stay in flight
-            wait_vm(nvm * (L::AHEAD - 2));
+            wait_vm(nvm * (AHEAD - 2));
             __syncthreads();
         } else {
             wait_vm(0);
@@ -489,20 +579,65 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ ga
         make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2v | ((uint32_t)h3 << 16));
 }
 
+// Device buffer for the fp16 images of a call's KV range, grown on demand, one per device (138 MB for 33792
+// positions).  Like the partial states, calls that overlap on one device share it and must be stream-ordered.
+static uint8_t* pf_image_buffer(size_t bytes, hipError_t* err) {
+    static std::mutex mu;
+    static uint8_t* buf[64] = {};
+    static size_t cap[64] = {};
+    int dev = 0;
+    if ((*err = hipGetDevice(&dev)) != hipSuccess) return nullptr;
+    if (dev < 0 || dev >= 64) {
+        *err = hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (cap[dev] < bytes) {
+        if (buf[dev] && (*err = hipFree(buf[dev])) != hipSuccess) return nullptr;  // hipFree waits for the device
+        buf[dev] = nullptr;
+        cap[dev] = 0;
+        const size_t want = (bytes + ((size_t)64 << 20) - 1) / ((size_t)64 << 20) * ((size_t)64 << 20);
+        if ((*err = hipMalloc(&buf[dev], want)) != hipSuccess) return nullptr;
+        cap[dev] = want;
+    }
+    return buf[dev];
+}
+
+template <int KVT>
+static void launch_prefill_pass(const float* qp, const qwa_kv_layer& kv, int nb, int p0, const uint8_t* img,
+                                int img_tiles, hipStream_t st) {
+    const dim3 grid((GRP * nb + PF_ROWS - 1) / PF_ROWS, NKV, PF_NS);
+    unsigned long long* prof = profile_slot(grid.x * grid.y * grid.z, st);
+    hipLaunchKernelGGL((k_prefill<KVT, PF_IMAGE>), grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0, img, img_tiles, prof);
+    profile_launched(prof, st);
+}
+
 hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
                           uint16_t* out16, hipStream_t st) {
+    const uint8_t* img = nullptr;
+    const int img_tiles = (p0 + B - 1) / PF_TILE + 1;
+    if (PF_IMAGE) {
+        hipError_t e = hipSuccess;
+        uint8_t* ib = pf_image_buffer((size_t)NKV * img_tiles * PF_IMG_BYTES, &e);
+        if (ib == nullptr) return e;
+        const dim3 grid(img_tiles, NKV);
+        if (kvt == QWA_KV_F16)
+            hipLaunchKernelGGL(k_pf_image<QWA_KV_F16>, grid, dim3(PF_THREADS), 0, st, kv, p0 + B - 1, img_tiles, ib);
+        else if (kvt == QWA_KV_Q8_0)
+            hipLaunchKernelGGL(k_pf_image<QWA_KV_Q8_0>, grid, dim3(PF_THREADS), 0, st, kv, p0 + B - 1, img_tiles, ib);
+        else
+            hipLaunchKernelGGL(k_pf_image<QWA_KV_Q4_0>, grid, dim3(PF_THREADS), 0, st, kv, p0 + B - 1, img_tiles, ib);
+        img = ib;
+    }
     for (int t0 = 0; t0 < B; t0 += PF_MAXB) {
         const int nb = min(PF_MAXB, B - t0);
         const float* qp = q + (size_t)t0 * NH * HD;
-        const dim3 grid((GRP * nb + PF_ROWS - 1) / PF_ROWS, NKV, PF_NS);
-        unsigned long long* prof = profile_slot(grid.x * grid.y * grid.z, st);
         if (kvt == QWA_KV_F16)
-            hipLaunchKernelGGL(k_prefill<QWA_KV_F16>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0, prof);
+            launch_prefill_pass<QWA_KV_F16>(qp, kv, nb, p0 + t0, img, img_tiles, st);
         else if (kvt == QWA_KV_Q8_0)
-            hipLaunchKernelGGL(k_prefill<QWA_KV_Q8_0>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0, prof);
+            launch_prefill_pass<QWA_KV_Q8_0>(qp, kv, nb, p0 + t0, img, img_tiles, st);
         else
-            hipLaunchKernelGGL(k_prefill<QWA_KV_Q4_0>, grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0 + t0, prof);
-        profile_launched(prof, st);
+            launch_prefill_pass<QWA_KV_Q4_0>(qp, kv, nb, p0 + t0, img, img_tiles, st);
         const int nrows = nb * NH;
         hipLaunchKernelGGL(k_pf_combine, dim3((nrows + 3) / 4), dim3(256), 0, st, gate + (size_t)t0 * NH * HD, nrows,
                            out16 + (size_t)t0 * NH * HD);
