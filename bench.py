@@ -192,6 +192,9 @@ def main():
         us = ms * 1000.0 / L
         extra["verify7_150k_us_per_layer"] = round(us, 3)
         extra["verify7_150k_gbs"] = round((n + 6) * BYTES_PER_POS[kvt] / (us * 1e-6) / 1e9, 1)
+        # the same 16 layers captured in one HIP graph, as an engine issues its step (no Python launch gaps)
+        ms = time_graph(torch, lambda: step(7), max(5, args.steps // 5))
+        extra["verify7_150k_us_per_layer_graph"] = round(ms * 1000.0 / L, 3)
         del layers
         torch.cuda.empty_cache()
         # C3: 7-query verify over Q4_0 32768 (16 layers)
@@ -202,6 +205,9 @@ def main():
         us = ms * 1000.0 / L
         extra["verify7_q4_32768_us_per_layer"] = round(us, 3)
         extra["verify7_q4_32768_gbs"] = round(n3 * 1152 / (us * 1e-6) / 1e9, 1)
+        ms = time_graph(torch, lambda: [ops.attn_decode_multi(q, gate, kv, ops.Q4_0, 32768, 7, work, out) for kv in l3],
+                        max(5, args.steps // 5))
+        extra["verify7_q4_32768_us_per_layer_graph"] = round(ms * 1000.0 / L, 3)
         del l3
         # C2: Q8_0 4096 decode with the new token's quantize-on-append (append + decode per layer)
         l2 = [fill_cache(ops, torch, ops.Q8_0, 4097, 3000 + i, 0.0) for i in range(L)]
@@ -214,6 +220,8 @@ def main():
                 ops.attn_decode_multi(q, gate, kv, ops.Q8_0, 4096, 1, work, out)
         ms = time_calls(torch, c2, max(5, args.steps // 5), 2)
         extra["decode_q8_4096_append_us_per_layer"] = round(ms * 1000.0 / L, 3)
+        ms = time_graph(torch, c2, max(5, args.steps // 5))
+        extra["decode_q8_4096_append_us_per_layer_graph"] = round(ms * 1000.0 / L, 3)
         del l2
         # C4: prefill chunk of 1024 tokens at p0 = 32768, Q8_0
         p0, B = 32768, 1024
