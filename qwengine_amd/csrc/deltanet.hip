@@ -287,7 +287,7 @@ constexpr int DN_TPW = 8 / DN_CW;       // 16-row key-dim tiles of the state per
 constexpr int DN_CP = 20;      // padded row (floats) of the transposed chunk tiles in LDS
 constexpr int DN_NCOEF = 704;  // per (chunk, head): T^T [16][20] | P^T [16][20] | gamma | E | c1 | c2
 struct DnRows {
-    float* conv;   // [B][10240] after SiLU
+    float* conv;   // [B][10240] after SiLU (only the v channels, 4096 .. 10239, are written)
     float* qn;     // [B][2048] L2-normalised q
     float* kn;     // [B][2048] L2-normalised k
     float* beta;   // [B][48]
@@ -317,11 +317,19 @@ size_t dn_work_bytes(int B) {
            sizeof(float);
 }
 
-// out[t][c] = silu(sum_k w[c][k] in(t - 3 + k)), in(i) = qkv[i][c] for i >= 0, else row 3 + i of the old window
+// Per token t, channel c (grid (DN_CH / 256, B)): conv[t][c] = silu(sum_k w[c][k] in(t - 3 + k)), in(i) = qkv[i][c]
+// for i >= 0, else row 3 + i of the old window.  The q and k channels (blocks 0 .. 15, two heads of 128 each) are
+// not written out: the block L2-normalises its two heads through LDS (wave w < 2: head 2 x + w, lane holding dims
+// lane and lane + 64) into qn / kn.  Block 0 also writes beta and the decay of token t.  Only the v channels reach
+// r.conv.
 __global__ void __launch_bounds__(256) k_dn_conv_rows(const float* __restrict__ qkv, const float* __restrict__ cs_old,
-                                                      const float* __restrict__ conv_w, float* __restrict__ out) {
+                                                      const float* __restrict__ conv_w, DnRows r,
+                                                      const float* __restrict__ beta_raw,
+                                                      const float* __restrict__ alpha_raw,
+                                                      const float* __restrict__ dt_bias,
+                                                      const float* __restrict__ ssm_a, float eps) {
+    __shared__ float sx[256];
     const int t = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= DN_CH) return;
     const float4 w = *reinterpret_cast<const float4*>(conv_w + (size_t)c * 4);
     float x[4];
 #pragma unroll
@@ -329,7 +337,28 @@ __global__ void __launch_bounds__(256) k_dn_conv_rows(const float* __restrict__ 
         const int i = t - 3 + k;
         x[k] = i >= 0 ? qkv[(size_t)i * DN_CH + c] : cs_old[(size_t)(3 + i) * DN_CH + c];
     }
-    out[(size_t)t * DN_CH + c] = dn_silu(w.x * x[0] + w.y * x[1] + w.z * x[2] + w.w * x[3]);
+    const float y = dn_silu(w.x * x[0] + w.y * x[1] + w.z * x[2] + w.w * x[3]);
+    if (c >= 2 * DN_QK) {
+        r.conv[(size_t)t * DN_CH + c] = y;
+        return;
+    }
+    sx[threadIdx.x] = y;
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave < 2) {
+        const int hc = 2 * blockIdx.x + wave;  // head of the q | k channels: q heads 0 .. 15, then k heads 0 .. 15
+        const float v0 = sx[128 * wave + lane], v1 = sx[128 * wave + lane + 64];
+        const float iv = 1.0f / fmaxf(sqrtf(wave_sum(v0 * v0 + v1 * v1)), eps);
+        float* d = (hc < DN_KH ? r.qn + hc * DN_HD : r.kn + (hc - DN_KH) * DN_HD) + (size_t)t * DN_QK;
+        d[lane] = v0 * iv;
+        d[lane + 64] = v1 * iv;
+    } else if (blockIdx.x == 0 && (int)threadIdx.x - 128 < DN_VH) {
+        const int h = threadIdx.x - 128;
+        const float a = alpha_raw[(size_t)t * DN_VH + h] + dt_bias[h];
+        const float sp = a > 20.0f ? a : logf(1.0f + expf(a));
+        r.beta[(size_t)t * DN_VH + h] = 1.0f / (1.0f + expf(-beta_raw[(size_t)t * DN_VH + h]));
+        r.decay[(size_t)t * DN_VH + h] = expf(sp * ssm_a[h]);
+    }
 }
 
 // the window after the B tokens (rows k = input B - 3 + k), into the other buffer
@@ -341,35 +370,6 @@ __global__ void __launch_bounds__(256) k_dn_conv_state(const float* __restrict__
     for (int k = 0; k < 3; k++) {
         const int i = B - 3 + k;
         cs_new[(size_t)k * DN_CH + c] = i >= 0 ? qkv[(size_t)i * DN_CH + c] : cs_old[(size_t)(3 + i) * DN_CH + c];
-    }
-}
-
-// per token: L2-normalised q and k of the 16 key heads (wave w: key heads w, w + 4, ...), beta and decay
-__global__ void __launch_bounds__(256) k_dn_prep_rows(DnRows r, const float* __restrict__ beta_raw,
-                                                      const float* __restrict__ alpha_raw,
-                                                      const float* __restrict__ dt_bias,
-                                                      const float* __restrict__ ssm_a, float eps) {
-    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int kh = wave; kh < DN_KH; kh += 4) {
-        const float* qs = r.conv + (size_t)t * DN_CH + kh * DN_HD;
-        const float* ks = qs + DN_QK;
-        const float q0 = qs[lane], q1 = qs[lane + 64], k0 = ks[lane], k1 = ks[lane + 64];
-        const float iq = 1.0f / fmaxf(sqrtf(wave_sum(q0 * q0 + q1 * q1)), eps);
-        const float ik = 1.0f / fmaxf(sqrtf(wave_sum(k0 * k0 + k1 * k1)), eps);
-        const float qa = q0 * iq, qb = q1 * iq, ka = k0 * ik, kb = k1 * ik;
-        float* qd = r.qn + (size_t)t * DN_QK + kh * DN_HD;
-        float* kd = r.kn + (size_t)t * DN_QK + kh * DN_HD;
-        qd[lane] = qa;
-        qd[lane + 64] = qb;
-        kd[lane] = ka;
-        kd[lane + 64] = kb;
-    }
-    if (threadIdx.x < DN_VH) {
-        const int h = threadIdx.x;
-        const float a = alpha_raw[(size_t)t * DN_VH + h] + dt_bias[h];
-        const float sp = a > 20.0f ? a : logf(1.0f + expf(a));
-        r.beta[(size_t)t * DN_VH + h] = 1.0f / (1.0f + expf(-beta_raw[(size_t)t * DN_VH + h]));
-        r.decay[(size_t)t * DN_VH + h] = expf(sp * ssm_a[h]);
     }
 }
 
@@ -658,9 +658,9 @@ hipError_t launch_dn_rows(const qwa_dn_params& p, const float* qkv, const float*
     const DnRows r = dn_rows_split(work, B);
     const float* cs_old = p.conv_state + (size_t)cin * 3 * DN_CH;
     float* cs_new = p.conv_state + (size_t)(cin ^ 1) * 3 * DN_CH;
-    hipLaunchKernelGGL(k_dn_conv_rows, dim3(DN_CH / 256, B), dim3(256), 0, st, qkv, cs_old, p.conv_w, r.conv);
+    hipLaunchKernelGGL(k_dn_conv_rows, dim3(DN_CH / 256, B), dim3(256), 0, st, qkv, cs_old, p.conv_w, r, beta_raw,
+                       alpha_raw, p.dt_bias, p.ssm_a, eps);
     hipLaunchKernelGGL(k_dn_conv_state, dim3(DN_CH / 256), dim3(256), 0, st, qkv, cs_old, B, cs_new);
-    hipLaunchKernelGGL(k_dn_prep_rows, dim3(B), dim3(256), 0, st, r, beta_raw, alpha_raw, p.dt_bias, p.ssm_a, eps);
     const int nch = (B + DN_CT - 1) / DN_CT;
     hipLaunchKernelGGL(k_dn_chunk_prep, dim3(DN_VH, nch), dim3(256), 0, st, r, B);
     hipLaunchKernelGGL(k_dn_chunk_rows, dim3(DN_VH, DN_RG), dim3(DN_CW * 64), 0, st, r, p.ssm_state, B, core_out);
