@@ -49,6 +49,10 @@ constexpr int VT_LD = PF_TILE + 8;               // V^T tile row stride (halves)
 #define QWA_PF_VD 3
 #endif
 constexpr int PF_VD = QWA_PF_VD;                 // V fragments in flight
+#ifndef QWA_PF_KPF
+#define QWA_PF_KPF 1
+#endif
+constexpr int PF_KPF = QWA_PF_KPF;               // score steps of K fragments read ahead (0: compiler's schedule)
 #ifndef QWA_PF_GROUP_BIT
 #define QWA_PF_GROUP_BIT 4
 #endif
@@ -448,15 +452,42 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
             for (int k4 = 0; k4 < PF_KT; k4++)
 #pragma unroll
                 for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            // swizzled unit (4 s + lg) ^ x = 4 (s ^ (x >> 2)) + (lg ^ (x & 3)): two lane bases, even / odd s
+            auto kfrag = [&](int s, int k4) {
+                return IMG ? lds_h8((s & 1 ? kimg_o : kimg_e) + (16 * k4) * HD + 32 * s)
+                           : lds_h8(Ks + (16 * k4 + i16) * KS_LD + 8 * lg + 32 * s);
+            };
+            if constexpr (PF_KPF > 0) {
+                // the K fragments of step s + PF_KPF are read while step s multiplies (scheduling barriers keep the
+                // compiler from sinking the reads next to their MFMAs)
+                h8 kf[PF_KPF + 1][PF_KT];
 #pragma unroll
-            for (int s = 0; s < 8; s++) {
+                for (int s = 0; s < PF_KPF; s++)
 #pragma unroll
-                for (int k4 = 0; k4 < PF_KT; k4++) {
-                    // swizzled unit (4 s + lg) ^ x = 4 (s ^ (x >> 2)) + (lg ^ (x & 3)): two lane bases, even / odd s
-                    const h8 a = IMG ? lds_h8((s & 1 ? kimg_o : kimg_e) + (16 * k4) * HD + 32 * s)
-                                     : lds_h8(Ks + (16 * k4 + i16) * KS_LD + 8 * lg + 32 * s);
+                    for (int k4 = 0; k4 < PF_KT; k4++) kf[s][k4] = kfrag(s, k4);
 #pragma unroll
-                    for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = mfma16(a, qb[rt][s], sc[rt][k4]);
+                for (int s = 0; s < 8; s++) {
+                    if (s + PF_KPF < 8) {
+#pragma unroll
+                        for (int k4 = 0; k4 < PF_KT; k4++) kf[(s + PF_KPF) % (PF_KPF + 1)][k4] = kfrag(s + PF_KPF, k4);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int k4 = 0; k4 < PF_KT; k4++)
+#pragma unroll
+                        for (int rt = 0; rt < PF_RT; rt++)
+                            sc[rt][k4] = mfma16(kf[s % (PF_KPF + 1)][k4], qb[rt][s], sc[rt][k4]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < 8; s++) {
+#pragma unroll
+                    for (int k4 = 0; k4 < PF_KT; k4++) {
+                        const h8 a = kfrag(s, k4);
+#pragma unroll
+                        for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = mfma16(a, qb[rt][s], sc[rt][k4]);
+                    }
                 }
             }
         };
