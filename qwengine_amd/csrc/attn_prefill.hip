@@ -333,8 +333,8 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
     __shared__ __attribute__((aligned(16))) _Float16 s_vt[IMG ? 1 : 2][IMG ? 8 : HD * VT_LD];
     const int t = threadIdx.x, lane = t & 63, i16 = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane((int)(t >> 6));
-    const int g = blockIdx.y, sp = blockIdx.z;
-    const int row0 = blockIdx.x * PF_ROWS;
+    const int bx = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
+    const int row0 = bx * PF_ROWS;
     const int nrows = GRP * B;
     // last key any row of the workgroup sees, and this split's tiles [tb, tb + nt) of the row block's range
     const int last_row = min(row0 + PF_ROWS, nrows) - 1;
