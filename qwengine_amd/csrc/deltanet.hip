@@ -628,19 +628,28 @@ k_dn_chunk_rows(DnRows r, float* __restrict__ state, int B,
             make_float4(st[m][0], st[m][1], st[m][2], st[m][3]);
 }
 
-// gated RMSNorm per (token, value head), fp16 out: grid (B, 48), 128 threads
-__global__ void __launch_bounds__(128) k_dn_gnorm_rows(const float* __restrict__ core, const float* __restrict__ z,
+// gated RMSNorm per (token, value head), fp16 out: grid (B), 256 threads; wave w normalises value heads w, w + 4,
+// ..., lane holding dims 2 lane, 2 lane + 1 (all loads of the token issued before the first reduction)
+__global__ void __launch_bounds__(256) k_dn_gnorm_rows(const float* __restrict__ core, const float* __restrict__ z,
                                                        const float* __restrict__ nw, float eps,
                                                        uint16_t* __restrict__ o16) {
-    __shared__ float red[2];
-    const int t = blockIdx.x, h = blockIdx.y, j = threadIdx.x, wave = j >> 6;
-    const size_t idx = (size_t)t * DN_VD + h * DN_HD + j;
-    const float v = core[idx];
-    const float sum = wave_sum(v * v);
-    if ((j & 63) == 0) red[wave] = sum;
-    __syncthreads();
-    const float rs = 1.0f / sqrtf((red[0] + red[1]) / DN_HD + eps);
-    o16[idx] = f2h_bits(v * rs * nw[j] * dn_silu(z[idx]));
+    constexpr int NHW = DN_VH / 4;  // heads per wave
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const float2 w = *reinterpret_cast<const float2*>(nw + 2 * lane);
+    float2 v[NHW], zz[NHW];
+#pragma unroll
+    for (int i = 0; i < NHW; i++) {
+        const size_t idx = (size_t)t * DN_VD + (wave + 4 * i) * DN_HD + 2 * lane;
+        v[i] = *reinterpret_cast<const float2*>(core + idx);
+        zz[i] = *reinterpret_cast<const float2*>(z + idx);
+    }
+#pragma unroll
+    for (int i = 0; i < NHW; i++) {
+        const float rs = 1.0f / sqrtf(wave_sum(v[i].x * v[i].x + v[i].y * v[i].y) / DN_HD + eps);
+        const uint32_t lo = f2h_bits(v[i].x * rs * w.x * dn_silu(zz[i].x));
+        const uint32_t hi = f2h_bits(v[i].y * rs * w.y * dn_silu(zz[i].y));
+        *reinterpret_cast<uint32_t*>(o16 + (size_t)t * DN_VD + (wave + 4 * i) * DN_HD + 2 * lane) = lo | (hi << 16);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------------ launchers
@@ -664,7 +673,7 @@ hipError_t launch_dn_rows(const qwa_dn_params& p, const float* qkv, const float*
     const int nch = (B + DN_CT - 1) / DN_CT;
     hipLaunchKernelGGL(k_dn_chunk_prep, dim3(DN_VH, nch), dim3(256), 0, st, r, B);
     hipLaunchKernelGGL(k_dn_chunk_rows, dim3(DN_VH, DN_RG), dim3(DN_CW * 64), 0, st, r, p.ssm_state, B, core_out);
-    hipLaunchKernelGGL(k_dn_gnorm_rows, dim3(B, DN_VH), dim3(128), 0, st, core_out, z, p.ssm_norm, eps, o16);
+    hipLaunchKernelGGL(k_dn_gnorm_rows, dim3(B), dim3(256), 0, st, core_out, z, p.ssm_norm, eps, o16);
     return hipGetLastError();
 }
 
