@@ -9,8 +9,8 @@ Secondary figures in the same line: 7-query verify at 150000 and 32768 positions
 and the 1024-token prefill chunk at p0 = 32768 (TFLOP/s against the fp16 MFMA dense peak).
 
 The CPU baseline (rank 0, N = 1 only) is the oracle's restatement of the reference CPU attention
-(src/reference/ref_model.cpp:195-219: fp32 8-lane FMA dots, double softmax, OpenMP over (token, head)) on a bounded
-sample of the same workload, timed on this box's host cores.
+(src/reference/ref_model.cpp:138-163: fp32 8-lane FMA dots, double softmax, OpenMP over (token, head)) on bounded
+samples of the configured shapes, timed on this box's host cores.
 """
 from __future__ import annotations
 
@@ -229,7 +229,8 @@ def main():
         qp = torch.randn((B, 24, 256), device="cuda").half().float()
         gp = torch.randn((B, 24, 256), device="cuda")
         o16 = torch.empty((B, 24, 256), dtype=torch.float16, device="cuda")
-        # the first call also sizes the library's image buffer: warm up, then the median of 4 groups of 5 calls
+        ops.attn_prefill_reserve(B, p0 + B)  # set-up: the stream's prefill workspace
+        # warm up, then the median of 4 groups of 5 calls
         time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 1, 3)
         ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 5, 0)
                     for _ in range(4))[1:3]
@@ -346,29 +347,63 @@ def consumer_extras(ops, torch, steps):
 
 
 def cpu_baseline(ops, torch, n):
-    """The reference CPU arithmetic (oracle mode 1) on one layer of the headline workload, host threads."""
+    """The reference CPU arithmetic (oracle mode 1: src/reference/ref_model.cpp:138-163, fp32 8-lane FMA dots, double
+    softmax and P.V, OpenMP over (token, head)) on this box's host threads, at the four shapes of the CPU plan: C1
+    (F16 4096, one query; the tensors of the C1 GPU parity test), C3 (7 queries over Q4_0 32768) and the headline
+    shape (Q4_0 150000) with 1 and 7 queries.  Quantized caches are dequantized to fp32 first, as the reference CPU
+    path holds fp32 K / V.  Each shape runs for about 3 s after one warm-up call."""
     import numpy as np
     import oracle as O
     sys.path.insert(0, os.path.join(HERE, "tests"))
+    from kvutil import c1_inputs
     print("[bench] cpu baseline", file=sys.stderr, flush=True)
-    kv = fill_cache(ops, torch, ops.Q4_0, n, 1000)
-    K = O.kv_load_rows(ops.Q4_0, kv.k.cpu().numpy(), kv.ks.cpu().numpy().view(np.uint16))
-    V = O.kv_load_rows(ops.Q4_0, kv.v.cpu().numpy(), kv.vs.cpu().numpy().view(np.uint16))
-    rng = np.random.default_rng(7)
-    q = rng.standard_normal((1, 24, 256)).astype(np.float32)
-    g = rng.standard_normal((1, 24, 256)).astype(np.float32)
     threads = O.max_threads()
-    O.attention(q, g, K, V, n - 1, 1, mode=1)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while reps < 3 or time.perf_counter() - t0 < 10.0:
-        O.attention(q, g, K, V, n - 1, 1, mode=1)
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    us = dt * 1e6
-    return {"value": round(n * 1152 / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "us_per_layer": round(us, 1),
-            "sample": f"{reps} decode calls over one 150000-position Q4_0 layer (cache dequantized to fp32), "
-                      f"oracle mode 1 = reference CPU arithmetic, {threads} OpenMP threads"}
+    rng = np.random.default_rng(7)
+    qn = rng.standard_normal((8, 24, 256)).astype(np.float32)
+    gn = rng.standard_normal((8, 24, 256)).astype(np.float32)
+
+    def host_cache(kvt, kv):
+        K = O.kv_load_rows(kvt, kv.k.cpu().numpy(), kv.ks.cpu().numpy().view(np.uint16) if kv.ks is not None else
+                           np.zeros((4, kv.capacity, 8), np.uint16))
+        V = O.kv_load_rows(kvt, kv.v.cpu().numpy(), kv.vs.cpu().numpy().view(np.uint16) if kv.vs is not None else
+                           np.zeros((4, kv.capacity, 8), np.uint16))
+        return K, V
+
+    def timed(q, g, K, V, pos0, nq, budget=3.0):
+        O.attention(q, g, K, V, pos0, nq, mode=1)  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while reps < 2 or time.perf_counter() - t0 < budget:
+            O.attention(q, g, K, V, pos0, nq, mode=1)
+            reps += 1
+        return (time.perf_counter() - t0) / reps, reps
+
+    shapes = {}
+    kv1, q1, g1 = c1_inputs()
+    K, V = host_cache(ops.F16, kv1)
+    dt, reps = timed(q1.cpu().numpy(), g1.cpu().numpy(), K, V, 4095, 1)
+    shapes["c1_f16_4096_nq1"] = {"us_per_layer": round(dt * 1e6, 1), "gbs": round(4096 * 4096 / dt / 1e9, 3),
+                                 "reps": reps}
+    del kv1, K, V
+    kv3 = fill_cache(ops, torch, ops.Q4_0, 32768 + 7, 2000)
+    K, V = host_cache(ops.Q4_0, kv3)
+    dt, reps = timed(qn[:7], gn[:7], K, V, 32768, 7)
+    shapes["c3_q4_0_32768_nq7"] = {"us_per_layer": round(dt * 1e6, 1), "gbs": round(32775 * 1152 / dt / 1e9, 3),
+                                   "reps": reps}
+    del kv3, K, V
+    kv = fill_cache(ops, torch, ops.Q4_0, n, 1000)
+    K, V = host_cache(ops.Q4_0, kv)
+    del kv
+    dt1, reps1 = timed(qn[:1], gn[:1], K, V, n - 1, 1)
+    shapes["c5_q4_0_150k_nq1"] = {"us_per_layer": round(dt1 * 1e6, 1), "gbs": round(n * 1152 / dt1 / 1e9, 3),
+                                  "reps": reps1}
+    dt, reps = timed(qn[:7], gn[:7], K, V, n - 7, 7)
+    shapes["c5_q4_0_150k_nq7"] = {"us_per_layer": round(dt * 1e6, 1), "gbs": round(n * 1152 / dt / 1e9, 3),
+                                  "reps": reps}
+    return {"value": shapes["c5_q4_0_150k_nq1"]["gbs"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_layer": shapes["c5_q4_0_150k_nq1"]["us_per_layer"], "shapes": shapes,
+            "sample": f"decode calls of the reference CPU arithmetic (oracle mode 1, {threads} OpenMP threads) over "
+                      "fp32 caches: C1 F16 4096 nq=1, C3 Q4_0 32768 nq=7, Q4_0 150000 nq=1 (value) and nq=7; about "
+                      "3 s per shape"}
 
 
 if __name__ == "__main__":

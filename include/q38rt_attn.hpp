@@ -167,6 +167,19 @@ inline void attn_prefill(const float* q, const float* gate, const KVLayer& kv, K
     detail::check(qwa_attn_prefill(q, gate, &l, (int)kvt, B, p0, out16, st), "attn_prefill");
 }
 
+// set-up of the drop-in attn_prefill (no reference counterpart): the workspace of `st`, reserved where the engine
+// reserves attn_work_bytes (src/runtime/engine.cpp:724)
+inline void attn_prefill_reserve(int max_B, int max_pos, hipStream_t st) {
+    detail::check(qwa_attn_prefill_reserve(max_B, max_pos, st), "attn_prefill_reserve");
+}
+inline void attn_prefill_release(hipStream_t st) { detail::check(qwa_attn_prefill_release(st), "attn_prefill_release"); }
+inline size_t attn_prefill_work_bytes(int B, int n_pos) { return qwa_attn_prefill_work_bytes(B, n_pos); }
+inline void attn_prefill(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int B, int p0,
+                         uint16_t* out16, void* work, size_t work_bytes, hipStream_t st) {
+    const qwa_kv_layer l = detail::c(kv);
+    detail::check(qwa_attn_prefill_ws(q, gate, &l, (int)kvt, B, p0, out16, work, work_bytes, st), "attn_prefill");
+}
+
 inline void attn_prefill_simple(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int B, int p0,
                                 uint16_t* out16, hipStream_t st) {
     const qwa_kv_layer l = detail::c(kv);

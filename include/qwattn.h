@@ -6,7 +6,8 @@
  * replaces.  Conventions:
  *   - all tensors are caller-owned device memory (out_host: host memory mapped for device access);
  *   - `stream` is a hipStream_t (NULL = the default stream); every call is asynchronous and stream-ordered;
- *   - no entry point allocates memory; the decode `work` buffer is sized by qwa_attn_work_bytes();
+ *   - no operator allocates memory; the decode `work` buffer is sized by qwa_attn_work_bytes(); the prefill workspace
+ *     is reserved once per stream at set-up (qwa_attn_prefill_reserve) or passed in (qwa_attn_prefill_ws);
  *   - the return value is a status code (QWA_OK = 0).  Invalid arguments are rejected before anything is launched
  *     (the reference aborts in the same situations, src/cuda/ops.cu:1002-1008); the C++ shim in q38rt_attn.hpp
  *     turns a nonzero status into abort() exactly like the reference.
@@ -108,10 +109,28 @@ int qwa_attn_prep_rows(const float* qg, const float* k, const float* v, const fl
                        int B, int p0, const float* rope, float eps, int kvt, const qwa_kv_layer* kv, float* q,
                        float* gate, void* stream);
 
-/* Replaces attn_prefill (src/cuda/prefill.cuh:59-60): causal attention of B queries at positions p0..p0+B-1 over
- * the cache [0, p0+B), output * sigmoid(gate) as fp16 bits [B][6144].  fp16 MFMA, fp32 accumulation. */
+/* Replaces attn_prefill (src/cuda/prefill.cuh:59-60, src/cuda/prefill.cu:899-908): causal attention of B queries at
+ * positions p0..p0+B-1 over the cache [0, p0+B), output * sigmoid(gate) as fp16 bits [B][6144].  fp16 MFMA, fp32
+ * accumulation.  The reference's signature has no work buffer; this kernel needs one (fp16 tile images of the KV
+ * range and split partial states), so the call uses the workspace reserved for its (device, stream) by
+ * qwa_attn_prefill_reserve and returns QWA_ERR_RANGE when there is none or the call exceeds it.  It allocates
+ * nothing, and calls on different streams use different workspaces. */
 int qwa_attn_prefill(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
                      uint16_t* out16, void* stream);
+
+/* Set-up for qwa_attn_prefill (no reference counterpart; the engine calls it where it reserves attn_work_bytes,
+ * src/runtime/engine.cpp:724): allocates (hipMalloc) the workspace of `stream` on the current device for calls with
+ * B <= max_B and p0 + B <= max_pos.  A second call for the same stream keeps a large-enough workspace or replaces a
+ * smaller one (after synchronising the stream).  qwa_attn_prefill_release frees it (after synchronising). */
+int qwa_attn_prefill_reserve(int max_B, int max_pos, void* stream);
+int qwa_attn_prefill_release(void* stream);
+
+/* attn_prefill with a caller-owned workspace (no reference counterpart): `work` of at least
+ * qwa_attn_prefill_work_bytes(B, p0 + B) bytes of device memory, used only by this call's stream-ordered kernels.
+ * Calls that run concurrently need distinct workspaces.  The size grows with B (up to 1024) and with p0 + B. */
+size_t qwa_attn_prefill_work_bytes(int B, int n_pos);
+int qwa_attn_prefill_ws(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
+                        uint16_t* out16, void* work, size_t work_bytes, void* stream);
 
 /* Replaces attn_prefill_simple (src/cuda/prefill.cuh:61-62): FP32 vector-ALU version kept for tests. */
 int qwa_attn_prefill_simple(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
@@ -119,7 +138,7 @@ int qwa_attn_prefill_simple(const float* q, const float* gate, const qwa_kv_laye
 
 /* Quantize-on-append of raw rows, without the norm / RoPE of prep: rows x [n][4][256] stored at positions pos0..
  * of every KV head, for K (xk) and V (xv); either may be NULL.  The store is the reference's kv_store_row
- * (src/cuda/common.cuh:199-228), exposed on its own so callers holding already-roped K can append them. */
+ * (src/cuda/common.cuh:54-80), exposed on its own so callers holding already-roped K can append them. */
 int qwa_kv_append(const float* xk, const float* xv, int pos0, int n, int kvt, const qwa_kv_layer* kv, void* stream);
 
 /* KV-cache lifecycle (no operator counterpart: the engine's resize, src/runtime/engine.cpp:248-275, parks "only the

@@ -134,7 +134,7 @@ def dequantize_q4_0(blocks) -> np.ndarray:
     return out
 
 
-# ---- split KV layout (src/cuda/ops.cuh:99-113, src/cuda/common.cuh:199-228) ----
+# ---- split KV layout (src/cuda/ops.cuh:99-113, src/cuda/common.cuh:54-80) ----
 def kv_value_bytes(kvt: int) -> int:
     return int(lib().qwo_kv_value_bytes(kvt))
 
@@ -166,7 +166,7 @@ def kv_load_rows(kvt: int, vals, scales) -> np.ndarray:
     return out
 
 
-# ---- attention (src/reference/ref_model.cpp:79-104,195-219) ----
+# ---- attention (src/reference/ref_model.cpp:23-48,138-163) ----
 def attention(q, gate, K, V, pos0: int, nq: int, mode: int = 0, threads: int = 0) -> np.ndarray:
     """q, gate [nq,24,256]; K, V dequantized [4, ld, 256] with ld >= pos0+nq.  mode 0 exact, 1 reference arithmetic."""
     q = _f32(q)

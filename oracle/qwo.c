@@ -155,7 +155,7 @@ void qwo_dequantize_q4_0(const uint8_t* blocks, float* y, int64_t n) {
 }
 
 /* ---------------------------------------------------------------------------------------------------------------
- * Split KV layout (src/cuda/ops.cuh:99-113, src/cuda/common.cuh:199-228): the same quantizer values as ggml's
+ * Split KV layout (src/cuda/ops.cuh:99-113, src/cuda/common.cuh:54-80): the same quantizer values as ggml's
  * blocks, regrouped per 256-value row into contiguous values + 8 fp16 scales, Q4_0 codes pairwise (2i low, 2i+1 high).
  * ------------------------------------------------------------------------------------------------------------- */
 size_t qwo_kv_value_bytes(int kvt) {
@@ -221,11 +221,11 @@ void qwo_kv_load_rows(int kvt, const uint8_t* vals, const uint16_t* scales, int6
 }
 
 /* ---------------------------------------------------------------------------------------------------------------
- * Gated attention: src/reference/ref_model.cpp:195-219 (+ :104 sigmoid).  Scores in double, softmax in double,
+ * Gated attention: src/reference/ref_model.cpp:138-163 (+ :48 sigmoid).  Scores in double, softmax in double,
  * P.V accumulated in double, normalised, then multiplied by sigmoid(gate).
  * ------------------------------------------------------------------------------------------------------------- */
 
-/* The reference CPU dot product (src/reference/ref_model.cpp:79-95): four 8-lane fp32 FMA accumulators over
+/* The reference CPU dot product (src/reference/ref_model.cpp:23-40): four 8-lane fp32 FMA accumulators over
  * 32-element steps, lanes summed pairwise in fp32, the 8 lanes then summed in double. */
 static float dot_ref(const float* a, const float* b, int n) {
 #ifdef QWO_HAVE_AVX2
@@ -255,10 +255,15 @@ static float dot_ref(const float* a, const float* b, int n) {
 #endif
 }
 
+/* Products of two floats are exact in double; four interleaved partial sums (n is a multiple of 4 here) let the
+ * compiler keep the sum in vector registers. */
 static double dot_exact(const float* a, const float* b, int n) {
-    double s = 0.0;
-    for (int i = 0; i < n; i++) s += (double)a[i] * (double)b[i];
-    return s;
+    double s[4] = {0.0, 0.0, 0.0, 0.0};
+    int i = 0;
+    for (; i + 4 <= n; i += 4)
+        for (int u = 0; u < 4; u++) s[u] += (double)a[i + u] * (double)b[i + u];
+    for (; i < n; i++) s[0] += (double)a[i] * (double)b[i];
+    return (s[0] + s[1]) + (s[2] + s[3]);
 }
 
 void qwo_attention(const float* q, const float* gate, const float* K, const float* V, int64_t ld, int pos0, int nq,

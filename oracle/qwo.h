@@ -8,8 +8,8 @@
  *   - fp16 conversion          : src/quant/quant_formats.h:29-78 (exact IEEE binary16, round to nearest even)
  *   - Q8_0 / Q4_0 quantizers   : src/quant/quant_ref.cpp:507-538 (ggml semantics, no FMA contraction)
  *   - Q8_0 / Q4_0 dequantizers : src/quant/quant_ref.cpp:302-319
- *   - split KV row layout      : src/cuda/ops.cuh:99-113, src/cuda/common.cuh:199-228
- *   - gated attention          : src/reference/ref_model.cpp:79-95 (dot_f32), :195-219 (softmax / P.V), :104 (sigmoid)
+ *   - split KV row layout      : src/cuda/ops.cuh:99-113, src/cuda/common.cuh:54-80
+ *   - gated attention          : src/reference/ref_model.cpp:23-40 (dot_f32), :138-163 (softmax / P.V), :48 (sigmoid)
  *   - q/k prep (RMSNorm, RoPE) : src/cuda/ops.cu:309-358, tests/kernels/test_ops.cu:260-272 (double precision)
  *   - RoPE tables              : src/cuda/prefill.cu:385-407
  *   - ActQ8 epilogue           : src/cuda/common.cuh:188-197

@@ -15,12 +15,11 @@
 //  * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16 (fp32 accumulation); P^T comes out of the S^T
 //    accumulator already in B-operand layout; online softmax in fp32 with a lazy rescale;
 //  * the causal key range of a row block is cut into PF_NS fixed splits (one workgroup each) so that the
-//    96 row blocks x 4 KV heads of a 1024-token chunk fill the chip; each split leaves a partial state (m, l, O) in
-//    a library-owned device buffer and k_pf_combine merges the splits in a fixed order, normalises, applies the
-//    sigmoid gate and writes fp16.  Chunks longer than PF_MAXB tokens run as several passes.
+//    96 row blocks x 4 KV heads of a 1024-token chunk fill the chip; each split leaves a partial state (m, l, O / l)
+//    in the caller's workspace and k_pf_combine merges the splits in a fixed order, applies the sigmoid gate and
+//    writes fp16.  Chunks longer than PF_MAXB tokens run as several passes.  Nothing here allocates: the images
+//    and partial states live in a workspace of prefill_work_bytes(B, p0 + B) bytes.
 #include <float.h>
-
-#include <mutex>
 
 #include "kv_operands.hpp"
 #include "launch.hpp"
@@ -60,11 +59,10 @@ constexpr int PF_GROUP_BIT = QWA_PF_GROUP_BIT;   // wave bit that tells the two 
 constexpr float PF_LOG2E = 1.4426950408889634f;
 constexpr float PF_RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maximum (natural-log units)
 
-// Partial softmax states of one pass: unnormalised O [split][row][HD] and (m, l) [split][row], row = token * NH +
-// head.  Library-owned (about 200 MB of device memory), so attn_prefill keeps the reference's signature without a
-// work buffer; calls that overlap on one device share it and must be stream-ordered.
-__device__ float4 pf_part_o[(size_t)PF_NS * PF_MAXROWS * HD / 4];
-__device__ float2 pf_part_ml[PF_NS * PF_MAXROWS];
+// Partial softmax states of one pass live in the caller's workspace: per split and output row
+// (row = token * NH + head, ps rows per split) O / l as fp32 [split][row][HD] and (m, l) as fp32 [split][row]; the
+// combine reweights them by l * exp(m - M).  (fp16 partials would halve these bytes but add a third fp16 rounding,
+// up to 2^-12 |O|, on top of the fp16 P and output of the reference's own MMA kernel.)
 
 // raw bytes of one tile in LDS, in the cache's own layout: K rows, V rows, K scales, V scales (8 fp16 per row)
 template <int KVT> struct PfRaw {
@@ -323,7 +321,7 @@ __device__ __forceinline__ float rows_sum(float x) {
 template <int KVT, bool IMG>
 __global__ void __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(PF_WPE, PF_WPE)))
 k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uint8_t* __restrict__ img, int img_tiles,
-          unsigned long long* prof) {
+          float4* __restrict__ part_o, float2* __restrict__ part_ml, int ps, unsigned long long* prof) {
     prof_start(prof);
     using L = PfRaw<KVT>;
     constexpr int NBUF = IMG ? PF_IMG_NBUF : L::NBUF;
@@ -560,118 +558,119 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
     }
     wait_vmcnt<0>();  // no direct-to-LDS load outlives the workgroup
 
-    // ---- partial state of this split: (m, l) and unnormalised O; lane holds dims 16 dt + 4 lg + i of row (rt, i16)
+    // ---- partial state of this split: (m, l) and O / l; lane holds dims 16 dt + 4 lg + i of row (rt, i16)
 #pragma unroll
     for (int rt = 0; rt < PF_RT; rt++) {
         const float lt = rows_sum(l[rt]);
         if (qpos[rt] < 0) continue;
         const int r = wrow0 + 16 * rt + i16, rr = (r / GRP) * NH + g * GRP + r % GRP;
-        const size_t prow = (size_t)sp * PF_MAXROWS + rr;
-        if (lg == 0) pf_part_ml[prow] = make_float2(m[rt], lt);
-        float4* dst = pf_part_o + prow * (HD / 4);
+        const size_t prow = (size_t)sp * ps + rr;
+        if (lg == 0) part_ml[prow] = make_float2(m[rt], lt);
+        const float il = lt > 0.0f ? 1.0f / lt : 0.0f;  // a split that saw no key leaves l = 0 and O = 0
+        float4* dst = part_o + prow * (HD / 4) + lg;
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
-            dst[4 * dt + lg] = make_float4(o[rt][dt][0], o[rt][dt][1], o[rt][dt][2], o[rt][dt][3]);
+            dst[4 * dt] = make_float4(o[rt][dt][0] * il, o[rt][dt][1] * il, o[rt][dt][2] * il, o[rt][dt][3] * il);
     }
     prof_end(prof);
 }
 
-// Merges the PF_NS partial states of each output row in split order, normalises, applies the sigmoid gate and
-// writes fp16: one wave per row (token * NH + head), 4 dims per lane.
+// Merges the PF_NS partial states of each output row in split order, applies the sigmoid gate and writes fp16: one
+// wave per row (token * NH + head), 4 dims per lane.  Split s weighs w_s = l_s exp(m_s - M); the row's output is
+// sum_s w_s (O_s / l_s) / sum_s w_s.
 __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ gate, int nrows,
-                                                      uint16_t* __restrict__ out16) {
+                                                    const float4* __restrict__ part_o,
+                                                    const float2* __restrict__ part_ml, int ps,
+                                                    uint16_t* __restrict__ out16) {
     const int rr = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (rr >= nrows) return;
     float2 ml[PF_NS];
+    float4 ov[PF_NS];
     float mx = -INFINITY;
 #pragma unroll
     for (int s = 0; s < PF_NS; s++) {
-        ml[s] = pf_part_ml[(size_t)s * PF_MAXROWS + rr];
+        ml[s] = part_ml[(size_t)s * ps + rr];
+        ov[s] = part_o[((size_t)s * ps + rr) * (HD / 4) + lane];
         mx = fmaxf(mx, ml[s].x);
     }
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float lsum = 0.0f;
+    float wsum = 0.0f;
 #pragma unroll
     for (int s = 0; s < PF_NS; s++) {
-        // a split that saw no visible key has m = -inf, l = 0, O = 0: weight 0
-        const float w = ml[s].x == -INFINITY ? 0.0f : fast_exp2((ml[s].x - mx) * PF_LOG2E);
-        const float4 v = pf_part_o[((size_t)s * PF_MAXROWS + rr) * (HD / 4) + lane];
-        acc.x += w * v.x;
-        acc.y += w * v.y;
-        acc.z += w * v.z;
-        acc.w += w * v.w;
-        lsum += w * ml[s].y;
+        const float w = ml[s].x == -INFINITY ? 0.0f : fast_exp2((ml[s].x - mx) * PF_LOG2E) * ml[s].y;
+        acc.x += w * ov[s].x;
+        acc.y += w * ov[s].y;
+        acc.z += w * ov[s].z;
+        acc.w += w * ov[s].w;
+        wsum += w;
     }
-    const float il = 1.0f / lsum;
+    const float iw = 1.0f / wsum;
     const float4 gv = *reinterpret_cast<const float4*>(gate + (size_t)rr * HD + 4 * lane);
-    const uint16_t h0 = f2h_bits(acc.x * il * sigmoid(gv.x)), h1 = f2h_bits(acc.y * il * sigmoid(gv.y));
-    const uint16_t h2v = f2h_bits(acc.z * il * sigmoid(gv.z)), h3 = f2h_bits(acc.w * il * sigmoid(gv.w));
+    const uint16_t h0 = f2h_bits(acc.x * iw * sigmoid(gv.x)), h1 = f2h_bits(acc.y * iw * sigmoid(gv.y));
+    const uint16_t h2v = f2h_bits(acc.z * iw * sigmoid(gv.z)), h3 = f2h_bits(acc.w * iw * sigmoid(gv.w));
     *reinterpret_cast<uint2*>(out16 + (size_t)rr * HD + 4 * lane) =
         make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2v | ((uint32_t)h3 << 16));
 }
 
-// Device buffer for the fp16 images of a call's KV range, grown on demand, one per device (138 MB for 33792
-// positions).  Like the partial states, calls that overlap on one device share it and must be stream-ordered.
-static uint8_t* pf_image_buffer(size_t bytes, hipError_t* err) {
-    static std::mutex mu;
-    static uint8_t* buf[64] = {};
-    static size_t cap[64] = {};
-    int dev = 0;
-    if ((*err = hipGetDevice(&dev)) != hipSuccess) return nullptr;
-    if (dev < 0 || dev >= 64) {
-        *err = hipErrorInvalidDevice;
-        return nullptr;
-    }
-    std::lock_guard<std::mutex> lock(mu);
-    if (cap[dev] < bytes) {
-        if (buf[dev] && (*err = hipFree(buf[dev])) != hipSuccess) return nullptr;  // hipFree waits for the device
-        buf[dev] = nullptr;
-        cap[dev] = 0;
-        const size_t want = (bytes + ((size_t)64 << 20) - 1) / ((size_t)64 << 20) * ((size_t)64 << 20);
-        if ((*err = hipMalloc(&buf[dev], want)) != hipSuccess) return nullptr;
-        cap[dev] = want;
-    }
-    return buf[dev];
+// Workspace layout of one call: the fp16 images of the KV range [0, p0 + B) (NKV x tiles x 32 KB; none when built
+// without images), then the (m, l) pairs and the partial O of one pass (PF_NS x ps rows, ps = NH x min(B, PF_MAXB)).
+struct PfWork {
+    uint8_t* img;
+    float2* ml;
+    float4* o;
+    int tiles, ps;
+    size_t bytes;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static PfWork pf_work_layout(uint8_t* base, int B, int n_pos) {
+    PfWork w;
+    w.tiles = (n_pos - 1) / PF_TILE + 1;
+    w.ps = NH * min(B, PF_MAXB);
+    const size_t img = PF_IMAGE ? align256((size_t)NKV * w.tiles * PF_IMG_BYTES) : 0;
+    const size_t ml = align256((size_t)PF_NS * w.ps * sizeof(float2));
+    const size_t o = (size_t)PF_NS * w.ps * HD * sizeof(float);
+    w.img = base;
+    w.ml = reinterpret_cast<float2*>(base + img);
+    w.o = reinterpret_cast<float4*>(base + img + ml);
+    w.bytes = img + ml + o;
+    return w;
 }
 
+size_t prefill_work_bytes(int B, int n_pos) { return pf_work_layout(nullptr, B, n_pos).bytes; }
+
 template <int KVT>
-static void launch_prefill_pass(const float* qp, const qwa_kv_layer& kv, int nb, int p0, const uint8_t* img,
-                                int img_tiles, hipStream_t st) {
+static void launch_prefill_pass(const float* qp, const qwa_kv_layer& kv, int nb, int p0, const PfWork& w,
+                                hipStream_t st) {
     const dim3 grid((GRP * nb + PF_ROWS - 1) / PF_ROWS, NKV, PF_NS);
     unsigned long long* prof = profile_slot(grid.x * grid.y * grid.z, st);
-    hipLaunchKernelGGL((k_prefill<KVT, PF_IMAGE>), grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0, img, img_tiles, prof);
+    hipLaunchKernelGGL((k_prefill<KVT, PF_IMAGE>), grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0, w.img, w.tiles, w.o,
+                       w.ml, w.ps, prof);
     profile_launched(prof, st);
 }
 
 hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
-                          uint16_t* out16, hipStream_t st) {
-    const uint8_t* img = nullptr;
-    const int img_tiles = (p0 + B - 1) / PF_TILE + 1;
+                          uint16_t* out16, void* work, hipStream_t st) {
+    const PfWork w = pf_work_layout(static_cast<uint8_t*>(work), B, p0 + B);
     if (PF_IMAGE) {
-        hipError_t e = hipSuccess;
-        uint8_t* ib = pf_image_buffer((size_t)NKV * img_tiles * PF_IMG_BYTES, &e);
-        if (ib == nullptr) return e;
-        const dim3 grid(img_tiles, NKV);
+        const dim3 grid(w.tiles, NKV);
         if (kvt == QWA_KV_F16)
-            hipLaunchKernelGGL(k_pf_image<QWA_KV_F16>, grid, dim3(PF_THREADS), 0, st, kv, p0 + B - 1, img_tiles, ib);
+            hipLaunchKernelGGL(k_pf_image<QWA_KV_F16>, grid, dim3(PF_THREADS), 0, st, kv, p0 + B - 1, w.tiles, w.img);
         else if (kvt == QWA_KV_Q8_0)
-            hipLaunchKernelGGL(k_pf_image<QWA_KV_Q8_0>, grid, dim3(PF_THREADS), 0, st, kv, p0 + B - 1, img_tiles, ib);
+            hipLaunchKernelGGL(k_pf_image<QWA_KV_Q8_0>, grid, dim3(PF_THREADS), 0, st, kv, p0 + B - 1, w.tiles, w.img);
         else
-            hipLaunchKernelGGL(k_pf_image<QWA_KV_Q4_0>, grid, dim3(PF_THREADS), 0, st, kv, p0 + B - 1, img_tiles, ib);
-        img = ib;
+            hipLaunchKernelGGL(k_pf_image<QWA_KV_Q4_0>, grid, dim3(PF_THREADS), 0, st, kv, p0 + B - 1, w.tiles, w.img);
     }
     for (int t0 = 0; t0 < B; t0 += PF_MAXB) {
         const int nb = min(PF_MAXB, B - t0);
         const float* qp = q + (size_t)t0 * NH * HD;
-        if (kvt == QWA_KV_F16)
-            launch_prefill_pass<QWA_KV_F16>(qp, kv, nb, p0 + t0, img, img_tiles, st);
-        else if (kvt == QWA_KV_Q8_0)
-            launch_prefill_pass<QWA_KV_Q8_0>(qp, kv, nb, p0 + t0, img, img_tiles, st);
-        else
-            launch_prefill_pass<QWA_KV_Q4_0>(qp, kv, nb, p0 + t0, img, img_tiles, st);
+        if (kvt == QWA_KV_F16) launch_prefill_pass<QWA_KV_F16>(qp, kv, nb, p0 + t0, w, st);
+        else if (kvt == QWA_KV_Q8_0) launch_prefill_pass<QWA_KV_Q8_0>(qp, kv, nb, p0 + t0, w, st);
+        else launch_prefill_pass<QWA_KV_Q4_0>(qp, kv, nb, p0 + t0, w, st);
         const int nrows = nb * NH;
         hipLaunchKernelGGL(k_pf_combine, dim3((nrows + 3) / 4), dim3(256), 0, st, gate + (size_t)t0 * NH * HD, nrows,
-                           out16 + (size_t)t0 * NH * HD);
+                           w.o, w.ml, w.ps, out16 + (size_t)t0 * NH * HD);
     }
     return hipGetLastError();
 }

@@ -1,8 +1,11 @@
-// C ABI (include/qwattn.h): argument validation, then the kernel launchers.  Nothing here allocates memory, except
-// the opt-in timing window (qwa_profile_begin), which keeps one stamp buffer for the life of the process.
+// C ABI (include/qwattn.h): argument validation, then the kernel launchers.  No operator call allocates memory.  Two
+// set-up calls do: qwa_attn_prefill_reserve (the per-stream prefill workspace, freed by qwa_attn_prefill_release)
+// and the opt-in timing window (qwa_profile_begin), which keeps one stamp buffer for the life of the process.
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "launch.hpp"
@@ -47,6 +50,25 @@ int check_src(const qwa_row_src* s, int n, const char* what, const char* fn) {
 }
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Prefill workspaces reserved at set-up, one per (device, stream): the drop-in attn_prefill keeps the reference's
+// signature (no work argument) and finds its stream's workspace here, so calls on different streams never share
+// scratch and no call allocates.
+struct PfReservation {
+    int dev;
+    void* stream;
+    void* ptr;
+    size_t bytes;
+    int max_B, max_pos;
+};
+std::mutex g_pf_mu;
+std::vector<PfReservation> g_pf;
+
+PfReservation* pf_find(int dev, void* stream) {
+    for (auto& r : g_pf)
+        if (r.dev == dev && r.stream == stream) return &r;
+    return nullptr;
+}
 
 // kernel timing window: each timed launch gets a slot of per-workgroup (start, end) stamps in a device buffer
 constexpr int PROF_MAX = 1024;     // launches per window
@@ -194,11 +216,94 @@ static int check_prefill(const float* q, const float* gate, const qwa_kv_layer* 
     return QWA_OK;
 }
 
+size_t qwa_attn_prefill_work_bytes(int B, int n_pos) {
+    if (B <= 0 || n_pos < B || n_pos > qwa::MAX_POS) return 0;
+    return qwa::prefill_work_bytes(B, n_pos);
+}
+
+int qwa_attn_prefill_ws(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
+                        uint16_t* out16, void* work, size_t work_bytes, void* stream) {
+    const char* fn = "attn_prefill_ws";
+    int st;
+    if ((st = check_prefill(q, gate, kv, kvt, B, p0, out16, fn))) return st;
+    if (work == nullptr) return fail(QWA_ERR_INVALID, "%s: null workspace", fn);
+    const size_t need = qwa::prefill_work_bytes(B, p0 + B);
+    if (work_bytes < need)
+        return fail(QWA_ERR_RANGE, "%s: workspace of %zu bytes, the call needs %zu", fn, work_bytes, need);
+    return from_hip(qwa::launch_prefill(q, gate, *kv, kvt, B, p0, out16, work, as_stream(stream)), fn);
+}
+
+int qwa_attn_prefill_reserve(int max_B, int max_pos, void* stream) {
+    const char* fn = "attn_prefill_reserve";
+    if (max_B <= 0 || max_pos < max_B || max_pos > qwa::MAX_POS)
+        return fail(QWA_ERR_RANGE, "%s: max_B %d, max_pos %d", fn, max_B, max_pos);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return from_hip(e, fn);
+    // the workspace covers every call with B <= max_B and p0 + B <= max_pos (its size grows with both)
+    const size_t need = qwa::prefill_work_bytes(max_B, max_pos);
+    std::lock_guard<std::mutex> lock(g_pf_mu);
+    PfReservation* r = pf_find(dev, stream);
+    if (r != nullptr && r->bytes >= need) {
+        r->max_B = std::max(r->max_B, max_B);
+        r->max_pos = std::max(r->max_pos, max_pos);
+        return QWA_OK;
+    }
+    void* p = nullptr;
+    if ((e = hipMalloc(&p, need)) != hipSuccess) return from_hip(e, fn);
+    if (r != nullptr) {
+        // a smaller workspace of this stream: release it once the stream's queued work is done
+        if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess || (e = hipFree(r->ptr)) != hipSuccess) {
+            (void)hipFree(p);
+            return from_hip(e, fn);
+        }
+        r->ptr = p;
+        r->bytes = need;
+        r->max_B = max_B;
+        r->max_pos = max_pos;
+    } else {
+        g_pf.push_back(PfReservation{dev, stream, p, need, max_B, max_pos});
+    }
+    return QWA_OK;
+}
+
+int qwa_attn_prefill_release(void* stream) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return from_hip(e, "attn_prefill_release");
+    std::lock_guard<std::mutex> lock(g_pf_mu);
+    for (size_t i = 0; i < g_pf.size(); i++) {
+        if (g_pf[i].dev == dev && g_pf[i].stream == stream) {
+            if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess) return from_hip(e, "attn_prefill_release");
+            e = hipFree(g_pf[i].ptr);
+            g_pf.erase(g_pf.begin() + (long)i);
+            return from_hip(e, "attn_prefill_release");
+        }
+    }
+    return QWA_OK;
+}
+
 int qwa_attn_prefill(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
                      uint16_t* out16, void* stream) {
+    const char* fn = "attn_prefill";
     int st;
-    if ((st = check_prefill(q, gate, kv, kvt, B, p0, out16, "attn_prefill"))) return st;
-    return from_hip(qwa::launch_prefill(q, gate, *kv, kvt, B, p0, out16, as_stream(stream)), "attn_prefill");
+    if ((st = check_prefill(q, gate, kv, kvt, B, p0, out16, fn))) return st;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return from_hip(e, fn);
+    void* work = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_pf_mu);
+        const PfReservation* r = pf_find(dev, stream);
+        if (r == nullptr)
+            return fail(QWA_ERR_RANGE, "%s: no workspace reserved for this stream on device %d "
+                                       "(call qwa_attn_prefill_reserve at set-up)", fn, dev);
+        if (B > r->max_B || p0 + B > r->max_pos)
+            return fail(QWA_ERR_RANGE, "%s: B = %d, p0 + B = %d beyond the stream's reservation (max_B %d, max_pos %d)",
+                        fn, B, p0 + B, r->max_B, r->max_pos);
+        work = r->ptr;
+    }
+    return from_hip(qwa::launch_prefill(q, gate, *kv, kvt, B, p0, out16, work, as_stream(stream)), fn);
 }
 
 int qwa_attn_prefill_simple(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,

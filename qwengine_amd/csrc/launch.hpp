@@ -55,8 +55,9 @@ hipError_t launch_dn_rows(const qwa_dn_params& p, const float* qkv, const float*
                           const float* alpha_raw, int B, int cin, float eps, void* work, float* core_out,
                           uint16_t* o16, hipStream_t st);
 
+size_t prefill_work_bytes(int B, int n_pos);
 hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
-                          uint16_t* out16, hipStream_t st);
+                          uint16_t* out16, void* work, hipStream_t st);
 hipError_t launch_prefill_simple(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,
                                  uint16_t* out16, hipStream_t st);
 

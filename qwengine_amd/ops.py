@@ -83,6 +83,11 @@ EXPORTS = {
                                                                   ctypes.POINTER(_KVLayerC)] + [ctypes.c_void_p] * 3),
     "qwa_attn_prefill": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC)] + [ctypes.c_int] * 3 +
                          [ctypes.c_void_p] * 2),
+    "qwa_attn_prefill_reserve": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "qwa_attn_prefill_release": (ctypes.c_int, [ctypes.c_void_p]),
+    "qwa_attn_prefill_work_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
+    "qwa_attn_prefill_ws": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC)] + [ctypes.c_int] * 3 +
+                            [ctypes.c_void_p] * 2 + [ctypes.c_size_t, ctypes.c_void_p]),
     "qwa_attn_prefill_simple": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC)] +
                                 [ctypes.c_int] * 3 + [ctypes.c_void_p] * 2),
     "qwa_kv_append": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.c_int] * 3 + [ctypes.POINTER(_KVLayerC),
@@ -319,9 +324,29 @@ def attn_prep_rows(qg, k, v, q_norm, k_norm, B: int, p0: int, rope, eps: float, 
 
 
 def attn_prefill(q, gate, kv: KVLayer, kvt, B: int, p0: int, out16, stream=None) -> None:
-    """src/cuda/prefill.cuh:59-60 (out16: fp16 [B, 6144])."""
+    """src/cuda/prefill.cuh:59-60 (out16: fp16 [B, 6144]).  Uses the workspace reserved for the stream by
+    attn_prefill_reserve (raises QwaError without one); allocates nothing."""
     _check(lib().qwa_attn_prefill(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), B, p0, _ptr(out16),
                                   _stream(stream)))
+
+
+def attn_prefill_reserve(max_B: int, max_pos: int, stream=None) -> None:
+    """Set-up: reserve the prefill workspace of the stream (calls with B <= max_B, p0 + B <= max_pos)."""
+    _check(lib().qwa_attn_prefill_reserve(max_B, max_pos, _stream(stream)))
+
+
+def attn_prefill_release(stream=None) -> None:
+    _check(lib().qwa_attn_prefill_release(_stream(stream)))
+
+
+def attn_prefill_work_bytes(B: int, n_pos: int) -> int:
+    return int(lib().qwa_attn_prefill_work_bytes(B, n_pos))
+
+
+def attn_prefill_ws(q, gate, kv: KVLayer, kvt, B: int, p0: int, out16, work, stream=None) -> None:
+    """attn_prefill with a caller-owned workspace tensor of at least attn_prefill_work_bytes(B, p0 + B) bytes."""
+    _check(lib().qwa_attn_prefill_ws(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), B, p0, _ptr(out16),
+                                     _ptr(work), work.numel() * work.element_size(), _stream(stream)))
 
 
 def attn_prefill_simple(q, gate, kv: KVLayer, kvt, B: int, p0: int, out16, stream=None) -> None:
@@ -367,7 +392,7 @@ def kv_unpack(src, kv: KVLayer, kvt, n_pos: int, stream=None) -> None:
 
 
 def kv_append(xk, xv, pos0: int, n: int, kvt, kv: KVLayer, stream=None) -> None:
-    """Quantize-on-append of raw K/V rows [n, 4, 256] (the row store of src/cuda/common.cuh:199-228)."""
+    """Quantize-on-append of raw K/V rows [n, 4, 256] (the row store of src/cuda/common.cuh:54-80)."""
     _check(lib().qwa_kv_append(_ptr(xk), _ptr(xv), pos0, n, _kvt(kvt), ctypes.byref(kv.c()), _stream(stream)))
 
 

@@ -7,11 +7,11 @@ directly in numpy float32 / float64 and shares no code with the C oracle. The fi
 * kv_quant_edge.npz -- rows of 256 floats. They cover the reference quantizer test's edge cases
   (tests/unit/test_quant_ref.cpp:119-122: an all-zero row, a single -5 spike, 1e-30 magnitudes, scales 1e-4..1e4
   times (1 + i % 7)), plus |x| ties, exact halves and outliers. For each of F16 / Q8_0 / Q4_0 the fixture stores
-  the split-layout bytes that kv_store_row must produce (src/cuda/common.cuh:199-228; the ggml rules of
+  the split-layout bytes that kv_store_row must produce (src/cuda/common.cuh:54-80; the ggml rules of
   src/quant/quant_ref.cpp:507-538).
 * attn_small.npz -- three small decode / verify cases (F16, Q8_0, Q4_0 with outlier keys). Each holds fp16-exact
   K/V/Q inputs, the gate logits, and the gated-attention output computed in float64 over the cache exactly as
-  stored (src/reference/ref_model.cpp:195-219, src/cuda/ops.cu:507-815).
+  stored (src/reference/ref_model.cpp:138-163, src/cuda/ops.cu:507-815).
 
 Usage: python tests/golden/make_golden.py   (rewrites both files; the output is deterministic)
 """

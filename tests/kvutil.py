@@ -54,3 +54,17 @@ def assert_close(got, ref, what="", max_abs=MAX_ABS, rel_l2=REL_L2):
     ma, rl = errors(got, ref)
     assert ma <= max_abs and rl <= rel_l2, f"{what}: max-abs {ma:.3e} (tol {max_abs}), rel-L2 {rl:.3e} (tol {rel_l2})"
     return ma, rl
+
+
+def c1_inputs(device="cuda"):
+    """BASELINE config 1 (the CPU reference's decode case): F16 KV cache of 4096 positions, K / V ~N(0,1) post-RoPE
+    cast to fp16 (round to nearest even, by the F16 append), q and gate logits ~N(0,1), one query at position 4095.
+    The GPU parity test and bench.py's CPU baseline use these same tensors."""
+    n = 4096
+    kv = ops.KVLayer.allocate(ops.F16, n, device=device)
+    K = seeded_normal((n, 4, 256), 501, device)
+    V = seeded_normal((n, 4, 256), 502, device)
+    ops.kv_append(K, V, 0, n, ops.F16, kv)
+    q = seeded_normal((1, 24, 256), 503, device)
+    gate = seeded_normal((1, 24, 256), 504, device)
+    return kv, q, gate

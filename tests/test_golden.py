@@ -1,6 +1,6 @@
 """The C oracle against the committed golden fixtures (tests/golden/make_golden.py: an independent numpy restatement
-of the reference's quantizers, src/quant/quant_ref.cpp:507-538 in the split layout of src/cuda/common.cuh:199-228,
-and of the float64 gated attention of src/reference/ref_model.cpp:195-219)."""
+of the reference's quantizers, src/quant/quant_ref.cpp:507-538 in the split layout of src/cuda/common.cuh:54-80,
+and of the float64 gated attention of src/reference/ref_model.cpp:138-163)."""
 import os
 
 import numpy as np

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 import qwengine_amd.ops as ops
-from kvutil import KVTS, KV_NAMES, assert_close, dequant_cache, make_cache, seeded_normal
+from kvutil import KVTS, KV_NAMES, assert_close, c1_inputs, dequant_cache, make_cache, seeded_normal
 
 pytestmark = pytest.mark.gpu
 
@@ -40,6 +40,17 @@ def test_decode_vs_oracle(gpu, oracle, kvt, n_pos):
     torch.cuda.synchronize()
     err = np.abs(out_s.cpu().numpy() - ref).max() / np.abs(ref).max()
     assert err <= 5e-5, err
+
+
+def test_config_c1_f16_4096(gpu, oracle):
+    """single-token decode over an F16 cache of 4096 positions, on the tensors the CPU baseline
+    times; against the float64 oracle and against the reference CPU arithmetic (oracle mode 1)."""
+    kv, q, gate = c1_inputs()
+    out = _decode(kv, q, gate, 4095, 1).cpu().numpy()
+    Kd, Vd = dequant_cache(kv, 4096)
+    qn, gn = q.cpu().numpy(), gate.cpu().numpy()
+    assert_close(out, oracle.attention(qn, gn, Kd, Vd, 4095, 1), "C1 vs float64 oracle")
+    assert_close(out, oracle.attention(qn, gn, Kd, Vd, 4095, 1, mode=1), "C1 vs reference CPU arithmetic")
 
 
 @pytest.mark.parametrize("kvt", KVTS, ids=lambda k: KV_NAMES[k])

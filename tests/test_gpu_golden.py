@@ -1,5 +1,5 @@
 """The HIP path against the committed golden fixtures (tests/golden/make_golden.py): quantize-on-append bytes
-(bit-exact, src/cuda/common.cuh:199-228), and decode / verify / prefill outputs (max-abs 2e-3, rel-L2 1e-3) on the
+(bit-exact, src/cuda/common.cuh:54-80), and decode / verify / prefill outputs (max-abs 2e-3, rel-L2 1e-3) on the
 fixture caches."""
 import os
 
