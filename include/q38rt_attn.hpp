@@ -161,6 +161,17 @@ inline void attn_prep_rows(const float* qg, const float* k, const float* v, cons
                   "attn_prep_rows");
 }
 
+// attn_decode_multi without a work buffer, for callers that cannot allocate (no reference counterpart): the library's
+// static per-GPU scratch; calls that overlap on one GPU race
+inline void attn_decode_multi_noalloc(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int pos0,
+                                      int nq, float* out, const ActQ8* oq, hipStream_t st, float* out_host = nullptr) {
+    const qwa_kv_layer l = detail::c(kv);
+    qwa_act_q8 q8{};
+    if (oq) q8 = qwa_act_q8{oq->q, oq->d, oq->s};
+    detail::check(qwa_attn_decode_multi_noalloc(q, gate, &l, (int)kvt, pos0, nq, out, oq ? &q8 : nullptr, st, out_host),
+                  "attn_decode_multi_noalloc");
+}
+
 inline void attn_prefill(const float* q, const float* gate, const KVLayer& kv, KVType kvt, int B, int p0,
                          uint16_t* out16, hipStream_t st) {
     const qwa_kv_layer l = detail::c(kv);

@@ -23,6 +23,8 @@
 // decode == decode_batch contract, src/cuda/ops.cuh:134-135).
 #include <float.h>
 
+#include <mutex>
+
 #include "kv_operands.hpp"
 #include "launch.hpp"
 
@@ -966,6 +968,44 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     hipLaunchKernelGGL(k_dec_combine, dim3(nq * NH, 4), dim3(256), 0, st, w, nsplit, gate, out, out_host, a,
                        oq != nullptr ? 1 : 0);
     return hipGetLastError();
+}
+
+// ---- allocation-free decode: the partial records live in a file-scope device array instead of a work argument.
+// Its size is dec_work_bytes() (25.6 MB), which covers every valid call (up to 8 queries, any context up to
+// MAX_POS).  Every GPU holds its own copy at its own address, fetched once per device with hipGetSymbolAddress; host
+// code never passes the array's name itself to a kernel.  All calls on one GPU share the array: calls that overlap
+// on that GPU (different streams, or different threads without ordering) race on it.  The records need no clearing:
+// every record a combine reads is written by the same call first.
+constexpr size_t DEC_SCRATCH_FLOATS = (size_t)NREC * NKV * MAXQ * GRP * REC;
+static __device__ __align__(256) float scratch[DEC_SCRATCH_FLOATS];
+
+size_t dec_scratch_bytes() { return DEC_SCRATCH_FLOATS * sizeof(float); }
+
+static float* scratch_ptr(hipError_t* err) {
+    constexpr int MAXDEV = 64;
+    static std::mutex mu;
+    static float* ptrs[MAXDEV] = {};
+    int dev = 0;
+    if ((*err = hipGetDevice(&dev)) != hipSuccess) return nullptr;
+    if (dev < 0 || dev >= MAXDEV) {
+        *err = hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptrs[dev] == nullptr) {
+        void* p = nullptr;
+        if ((*err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return nullptr;
+        ptrs[dev] = static_cast<float*>(p);
+    }
+    return ptrs[dev];
+}
+
+hipError_t launch_decode_noalloc(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int pos0, int nq,
+                                 float* out, const qwa_act_q8* oq, float* out_host, hipStream_t st) {
+    hipError_t e = hipSuccess;
+    float* w = scratch_ptr(&e);
+    if (w == nullptr) return e;
+    return launch_decode(q, gate, kv, kvt, pos0, nq, w, out, oq, out_host, st);
 }
 
 }  // namespace qwa

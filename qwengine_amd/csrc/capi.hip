@@ -143,19 +143,38 @@ size_t qwa_attn_work_bytes(int n_pos) {
 
 int qwa_attn_max_positions(void) { return qwa::MAX_POS; }
 
-int qwa_attn_decode_multi(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int pos0, int nq,
-                          void* work, float* out, const qwa_act_q8* oq, void* stream, float* out_host) {
-    const char* fn = "attn_decode_multi";
+static int check_decode(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int pos0, int nq,
+                        float* out, const qwa_act_q8* oq, const char* fn) {
     int st;
     if (nq < 1 || nq > qwa::MAXQ) return fail(QWA_ERR_INVALID, "%s: %d queries (1..%d)", fn, nq, qwa::MAXQ);
     if ((st = check_kv(kv, kvt, fn))) return st;
-    if (!q || !gate || !work || !out) return fail(QWA_ERR_INVALID, "%s: null pointer", fn);
+    if (!q || !gate || !out) return fail(QWA_ERR_INVALID, "%s: null pointer", fn);
     if (oq && (!oq->q || !oq->d || !oq->s)) return fail(QWA_ERR_INVALID, "%s: incomplete ActQ8 output", fn);
     if (pos0 < 0 || (long)pos0 + nq > qwa::MAX_POS)
         return fail(QWA_ERR_RANGE, "%s: context beyond %d positions", fn, qwa::MAX_POS);
     if ((long)pos0 + nq > kv->capacity)
         return fail(QWA_ERR_RANGE, "%s: positions up to %d beyond the cache capacity %d", fn, pos0 + nq, kv->capacity);
+    return QWA_OK;
+}
+
+int qwa_attn_decode_multi(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int pos0, int nq,
+                          void* work, float* out, const qwa_act_q8* oq, void* stream, float* out_host) {
+    const char* fn = "attn_decode_multi";
+    int st;
+    if ((st = check_decode(q, gate, kv, kvt, pos0, nq, out, oq, fn))) return st;
+    if (!work) return fail(QWA_ERR_INVALID, "%s: null pointer", fn);
     return from_hip(qwa::launch_decode(q, gate, *kv, kvt, pos0, nq, work, out, oq, out_host, as_stream(stream)), fn);
+}
+
+int qwa_attn_decode_multi_noalloc(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int pos0, int nq,
+                                  float* out, const qwa_act_q8* oq, void* stream, float* out_host) {
+    const char* fn = "attn_decode_multi_noalloc";
+    int st;
+    if ((st = check_decode(q, gate, kv, kvt, pos0, nq, out, oq, fn))) return st;
+    if (qwa::dec_work_bytes(pos0 + nq) > qwa::dec_scratch_bytes())
+        return fail(QWA_ERR_RANGE, "%s: the call needs %zu bytes of scratch, the library holds %zu", fn,
+                    qwa::dec_work_bytes(pos0 + nq), qwa::dec_scratch_bytes());
+    return from_hip(qwa::launch_decode_noalloc(q, gate, *kv, kvt, pos0, nq, out, oq, out_host, as_stream(stream)), fn);
 }
 
 int qwa_attn_decode(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int n_pos, void* work,

@@ -72,6 +72,9 @@ EXPORTS = {
                                                                ctypes.POINTER(_ActQ8C), ctypes.c_void_p]),
     "qwa_attn_decode_multi": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC)] + [ctypes.c_int] * 3 +
                               [ctypes.c_void_p] * 2 + [ctypes.POINTER(_ActQ8C), ctypes.c_void_p, ctypes.c_void_p]),
+    "qwa_attn_decode_multi_noalloc": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC)] +
+                                      [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.POINTER(_ActQ8C), ctypes.c_void_p,
+                                                            ctypes.c_void_p]),
     "qwa_attn_decode_simple": (ctypes.c_int, [ctypes.c_void_p] * 2 + [ctypes.POINTER(_KVLayerC), ctypes.c_int,
                                                                       ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
                                                                       ctypes.POINTER(_ActQ8C), ctypes.c_void_p]),
@@ -297,6 +300,14 @@ def attn_decode_multi(q, gate, kv: KVLayer, kvt, pos0: int, nq: int, work, out, 
     """src/cuda/ops.cuh:136-137."""
     _check(lib().qwa_attn_decode_multi(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), pos0, nq, _ptr(work),
                                        _ptr(out), _act(oq), _stream(stream), _ptr(out_host)))
+
+
+def attn_decode_multi_noalloc(q, gate, kv: KVLayer, kvt, pos0: int, nq: int, out, oq: ActQ8 | None = None,
+                              stream=None, out_host=None) -> None:
+    """attn_decode_multi on the library's static scratch: no work argument, nothing allocated (no reference
+    counterpart).  Calls that overlap on one GPU race on that scratch."""
+    _check(lib().qwa_attn_decode_multi_noalloc(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), pos0, nq,
+                                               _ptr(out), _act(oq), _stream(stream), _ptr(out_host)))
 
 
 def attn_decode_simple(q, gate, kv: KVLayer, kvt, n_pos: int, work, out, oq: ActQ8 | None = None,
