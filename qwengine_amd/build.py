@@ -6,7 +6,9 @@ from __future__ import annotations
 
 import concurrent.futures
 import os
+import shutil
 import subprocess
+import tempfile
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -41,8 +43,8 @@ def _hipcc() -> str:
     return "hipcc"
 
 
-def _compile(src: str, extra: list[str]) -> str:
-    obj = os.path.join(OUT_DIR, os.path.splitext(src)[0] + ".o")
+def _compile(src: str, extra: list[str], obj_dir: str) -> str:
+    obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
     cmd = [_hipcc(), *HIPCC_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -50,24 +52,26 @@ def _compile(src: str, extra: list[str]) -> str:
     return obj
 
 
-def build(verbose: bool = False, extra: list[str] | None = None) -> str:
+def build(verbose: bool = False, extra: list[str] | None = None, out: str | None = None) -> str:
+    """Compile every source and link the library (to ``out``, default qwengine_amd/_lib/libqwattn.so)."""
     os.makedirs(OUT_DIR, exist_ok=True)
     extra = extra or []
     workers = min(len(SOURCES), max(1, (os.cpu_count() or 4) // 2), 8)
+    target = out or LIB
+    obj_dir = tempfile.mkdtemp(prefix="qwattn_obj_")
     with concurrent.futures.ThreadPoolExecutor(workers) as ex:
-        objs = list(ex.map(lambda s: _compile(s, extra), SOURCES))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda s: _compile(s, extra, obj_dir), SOURCES))
+    tmp = target + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-L/opt/rocm/lib", "-lhipblaslt",
            "-Wl,-rpath,/opt/rocm/lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-4000:]}")
-    os.replace(tmp, LIB)
-    for o in objs:
-        os.remove(o)
+    os.replace(tmp, target)
+    shutil.rmtree(obj_dir, ignore_errors=True)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {target}")
+    return target
 
 
 if __name__ == "__main__":

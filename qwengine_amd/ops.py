@@ -20,7 +20,9 @@ F16, Q8_0, Q4_0 = 0, 1, 2
 KV_TYPES = {"f16": F16, "q8_0": Q8_0, "q4_0": Q4_0}
 N_HEAD, N_KV, HEAD_DIM, GROUP = 24, 4, 256, 6
 
-_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libqwattn.so")
+# QWA_LIBRARY selects another build of the same library (e.g. one compiled with different tuning macros)
+_LIB_PATH = os.environ.get("QWA_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib",
+                                                          "libqwattn.so")
 _lib = None
 
 

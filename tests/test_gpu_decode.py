@@ -159,3 +159,67 @@ def test_config_c5_long_decode_q4_150000(gpu, oracle, nq):
     Kd, Vd = dequant_cache(kv, n)
     ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, pos0, nq)
     assert_close(out.cpu().numpy(), ref, f"C5 nq={nq}")
+
+
+@pytest.mark.parametrize("kvt", [ops.Q4_0, ops.F16], ids=lambda k: KV_NAMES[k])
+def test_decode_mapped_host_copy(gpu, kvt):
+    """out_host (src/cuda/ops.cuh:136-137): the outputs are also written to mapped pinned host memory, fenced
+    system-wide before the kernel ends, so they equal the device rows once the stream is synchronised; with the ActQ8
+    epilogue at the same time."""
+    nq, pos0 = 7, 2000
+    kv, _, _ = make_cache(kvt, pos0 + nq, pos0 + nq, seed=41)
+    q, gate = _qg(nq, 43)
+    work = torch.empty(ops.attn_work_bytes(pos0 + nq) // 4 + 1, dtype=torch.float32, device="cuda")
+    out = torch.empty((nq, 24, 256), device="cuda")
+    host = torch.full((nq, 24, 256), float("nan"), pin_memory=True)
+    oq = ops.ActQ8.allocate(nq * 6144)
+    ops.attn_decode_multi(q, gate, kv, kvt, pos0, nq, work, out, oq, out_host=host)
+    torch.cuda.synchronize()
+    assert torch.equal(host, out.cpu())
+    assert torch.equal(out, _decode(kv, q, gate, pos0, nq))
+
+
+def test_decode_calls_on_two_streams(gpu):
+    """Decode calls queued on two streams at once, each with its own work buffer, give the bits of the same calls
+    made one after the other (the merge counters of concurrent calls are separate)."""
+    kvt = ops.Q4_0
+    cases = []
+    for i, (n, nq) in enumerate(((30000, 1), (12000, 7))):
+        kv, _, _ = make_cache(kvt, n + nq, n + nq, seed=51 + i)
+        q, gate = _qg(nq, 53 + i)
+        cases.append((kv, q, gate, n, nq))
+    want = [_decode(kv, q, g, n, nq) for kv, q, g, n, nq in cases]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    works = [torch.empty(ops.attn_work_bytes(n + nq) // 4 + 1, dtype=torch.float32, device="cuda")
+             for _, _, _, n, nq in cases]
+    outs = [torch.empty_like(w) for w in want]
+    torch.cuda.synchronize()
+    for rep in range(5):
+        for s, (kv, q, g, n, nq), w, o in zip(streams, cases, works, outs):
+            ops.attn_decode_multi(q, g, kv, kvt, n, nq, w, o, stream=s)
+        torch.cuda.synchronize()
+        for o, w in zip(outs, want):
+            assert torch.equal(o, w), rep
+
+
+def test_decode_in_hip_graph(gpu):
+    """A decode step captured into a HIP graph (the engine's decode step): every replay, with eager decode calls in
+    between, gives the eager bits."""
+    kvt, n, nq = ops.Q4_0, 9000, 3
+    kv, _, _ = make_cache(kvt, n + nq, n + nq, seed=61)
+    q, gate = _qg(nq, 63)
+    want = _decode(kv, q, gate, n, nq)
+    work = torch.empty(ops.attn_work_bytes(n + nq) // 4 + 1, dtype=torch.float32, device="cuda")
+    out = torch.empty_like(want)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        ops.attn_decode_multi(q, gate, kv, kvt, n, nq, work, out, stream=s)
+    for rep in range(4):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+        assert torch.equal(_decode(kv, q, gate, n - 5, nq), _decode(kv, q, gate, n - 5, nq))
+    del g
