@@ -74,5 +74,25 @@ def build(verbose: bool = False, extra: list[str] | None = None, out: str | None
     return target
 
 
+SHIM_E2E_SRC = os.path.join(ROOT, "tests", "shim_e2e.cpp")
+SHIM_E2E = os.path.join(ROOT, "tests", "_build", "shim_e2e")
+
+
+def build_shim_e2e(verbose: bool = False) -> str:
+    """Host-only C++ program that drives the library through include/q38rt_attn.hpp (the GPU test of the drop-in
+    C++ boundary).  Built here, beside the library, so GPU runs only execute it."""
+    os.makedirs(os.path.dirname(SHIM_E2E), exist_ok=True)
+    cmd = ["g++", "-std=c++17", "-O2", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"), "-I",
+           "/opt/rocm/include", SHIM_E2E_SRC, "-o", SHIM_E2E, "-L", OUT_DIR, "-lqwattn", "-L/opt/rocm/lib",
+           "-lamdhip64", "-Wl,-rpath,$ORIGIN/../../qwengine_amd/_lib", "-Wl,-rpath,/opt/rocm/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"shim_e2e build failed:\n{r.stderr[-4000:]}")
+    if verbose:
+        print(f"built {SHIM_E2E}")
+    return SHIM_E2E
+
+
 if __name__ == "__main__":
     build(verbose=True, extra=sys.argv[1:])
+    build_shim_e2e(verbose=True)
