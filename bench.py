@@ -317,7 +317,8 @@ def consumer_extras(ops, torch, steps):
     ops.quantize_act_q8(x, K, 1, a)
     y = torch.empty(N, device="cuda")
     rng = np.random.default_rng(0)
-    for fmt, name in ((ops.W_Q4_K, "q4_k"), (ops.W_IQ4_XS, "iq4_xs")):
+    for fmt, name in ((ops.W_Q4_K, "q4_k"), (ops.W_IQ4_XS, "iq4_xs"), (ops.W_IQ3_S, "iq3_s"), (ops.W_IQ2_XS, "iq2_xs"),
+                      (ops.W_IQ2_XXS, "iq2_xxs"), (ops.W_IQ2_S, "iq2_s")):
         rb = ops.w_row_bytes(fmt, K)
         Wn = rng.integers(0, 256, (N, rb), dtype=np.uint8)
         blocks = Wn.reshape(N, K // 256, rb // (K // 256))

@@ -229,10 +229,16 @@ int qwa_deltanet_rows(const qwa_dn_params* p, const float* qkv, const float* z, 
 /* ---- Consumers of the attention output: decode GEMV over ActQ8 activations, prefill weight dequantizer --------- */
 
 /* Weight formats, the reference's QuantFormat values (include/q38rt/q38rt_types.h:36-66), ggml block layouts
- * (src/quant/quant_formats.h:92-104).  The grid formats (IQ1_S / IQ1_M / IQ2_* / IQ3_*) are not supported here. */
+ * (src/quant/quant_formats.h:92-104).  Of the grid formats, IQ2_XXS / IQ2_XS / IQ2_S / IQ3_XXS / IQ3_S are supported
+ * (the formats of the model's attention output projection); IQ1_S / IQ1_M are not. */
 #define QWA_W_Q2_K 10
 #define QWA_W_Q4_K 12
 #define QWA_W_Q6_K 14
+#define QWA_W_IQ2_XXS 16
+#define QWA_W_IQ2_XS 17
+#define QWA_W_IQ3_XXS 18
+#define QWA_W_IQ3_S 21
+#define QWA_W_IQ2_S 22
 #define QWA_W_IQ4_XS 23
 #define QWA_W_BF16 30
 

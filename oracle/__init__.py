@@ -75,6 +75,8 @@ def lib():
                                ctypes.c_float, _f32p, _f32p, _f32p]
     L.qwo_w_row_bytes.restype = ctypes.c_size_t
     L.qwo_w_row_bytes.argtypes = [ctypes.c_int, _i64]
+    L.qwo_iq_grid.restype = ctypes.c_uint64
+    L.qwo_iq_grid.argtypes = [ctypes.c_int, ctypes.c_int]
     L.qwo_w_dequant_row.restype = ctypes.c_int
     L.qwo_w_dequant_row.argtypes = [ctypes.c_int, _u8p, _f32p, _i64]
     L.qwo_gemv_ref.restype = ctypes.c_int
@@ -258,6 +260,15 @@ def max_threads() -> int:
 
 # ---- weight formats of the output-projection consumer (src/quant/quant_ref.cpp:24-101,281-299) ----
 W_Q2_K, W_Q4_K, W_Q6_K, W_IQ4_XS, W_BF16 = 10, 12, 14, 23, 30
+# the i-quant grid formats (src/quant/quant_ref.cpp:105-222)
+W_IQ2_XXS, W_IQ2_XS, W_IQ3_XXS, W_IQ3_S, W_IQ2_S = 16, 17, 18, 21, 22
+IQ_TABLES = {"IQ2XXS": (0, 256, 8), "IQ2XS": (1, 512, 8), "IQ2S": (2, 1024, 8), "IQ3XXS": (3, 256, 4), "IQ3S": (4, 512, 4)}
+
+
+def iq_grid_bytes(name: str) -> bytes:
+    """The expanded byte table of an i-quant codebook (entries little-endian, bytes_per_entry each)."""
+    t, n, nb = IQ_TABLES[name]
+    return b"".join(int(lib().qwo_iq_grid(t, i)).to_bytes(8, "little")[:nb] for i in range(n))
 
 
 def w_row_bytes(fmt: int, K: int) -> int:

@@ -515,7 +515,100 @@ size_t qwo_w_row_bytes(int fmt, int64_t K) {
         case QWO_W_Q4_K: return (size_t)nb * 144;
         case QWO_W_Q6_K: return (size_t)nb * 210;
         case QWO_W_IQ4_XS: return (size_t)nb * 136;
+        case QWO_W_IQ2_XXS: return (size_t)nb * 66;
+        case QWO_W_IQ2_XS: return (size_t)nb * 74;
+        case QWO_W_IQ2_S: return (size_t)nb * 82;
+        case QWO_W_IQ3_XXS: return (size_t)nb * 98;
+        case QWO_W_IQ3_S: return (size_t)nb * 110;
         default: return 0;
+    }
+}
+
+/* ---- i-quant grid formats (src/quant/quant_ref.cpp:105-222) -----------------------------------------------------
+ * Codebooks from the level-index code words of iq_grids.inc (pinned against the reference's byte tables by their
+ * SHA-256).  Sign bytes of IQ2_XXS / IQ2_XS / IQ3_XXS come from a 7-bit index whose 8th bit makes the count of
+ * negative signs even (ksigns_iq2xs of ggml, src/quant/iq_tables.inc:8-17). */
+#define IQ_TABLE static const
+#include "iq_grids.inc"
+#undef IQ_TABLE
+
+static uint64_t iq_expand(const uint16_t* codes, const uint8_t* levels, int bits, int nbytes, int idx) {
+    uint64_t e = 0;
+    for (int j = 0; j < nbytes; j++) e |= (uint64_t)levels[(codes[idx] >> (bits * j)) & ((1 << bits) - 1)] << (8 * j);
+    return e;
+}
+
+uint64_t qwo_iq_grid(int table, int idx) {
+    switch (table) {
+        case 0: return idx >= 0 && idx < IQ2XXS_N ? iq_expand(IQ2XXS_CODES, IQ2XXS_LEVELS, IQ2XXS_BITS, 8, idx) : 0;
+        case 1: return idx >= 0 && idx < IQ2XS_N ? iq_expand(IQ2XS_CODES, IQ2XS_LEVELS, IQ2XS_BITS, 8, idx) : 0;
+        case 2: return idx >= 0 && idx < IQ2S_N ? iq_expand(IQ2S_CODES, IQ2S_LEVELS, IQ2S_BITS, 8, idx) : 0;
+        case 3: return idx >= 0 && idx < IQ3XXS_N ? iq_expand(IQ3XXS_CODES, IQ3XXS_LEVELS, IQ3XXS_BITS, 4, idx) : 0;
+        case 4: return idx >= 0 && idx < IQ3S_N ? iq_expand(IQ3S_CODES, IQ3S_LEVELS, IQ3S_BITS, 4, idx) : 0;
+        default: return 0;
+    }
+}
+
+static uint8_t iq_signs7(unsigned s7) {
+    s7 &= 127;
+    return (uint8_t)(s7 | ((unsigned)(__builtin_popcount(s7) & 1) << 7));
+}
+
+static uint32_t w_u32(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24); }
+
+/* 8 weights = db * grid byte j * (sign bit j ? -1 : 1) */
+static void iq_put8(float* y, float db, uint64_t grid, uint8_t signs) {
+    for (int j = 0; j < 8; j++) y[j] = db * (float)((grid >> (8 * j)) & 255) * ((signs >> j) & 1 ? -1.f : 1.f);
+}
+
+static void w_dequant_iq(int fmt, const uint8_t* blk, float* out) {
+    const float d = w_h(blk);
+    if (fmt == QWO_W_IQ2_XXS) { /* d | per 32 weights: 4 grid indices (bytes), then 4 x 7 sign bits | 4-bit scale */
+        for (int ib = 0; ib < 8; ib++) {
+            const uint8_t* q = blk + 2 + 8 * ib;
+            const uint32_t a1 = w_u32(q + 4);
+            const float db = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
+            for (int l = 0; l < 4; l++) iq_put8(out + 32 * ib + 8 * l, db, qwo_iq_grid(0, q[l]), iq_signs7(a1 >> (7 * l)));
+        }
+    } else if (fmt == QWO_W_IQ2_XS) { /* d | qs[32] u16 (9-bit index | 7 sign bits) | scales[8]: two 4-bit per 32 */
+        for (int ib = 0; ib < 8; ib++) {
+            const uint8_t sc = blk[66 + ib];
+            const float db[2] = {d * (0.5f + (float)(sc & 15)) * 0.25f, d * (0.5f + (float)(sc >> 4)) * 0.25f};
+            for (int l = 0; l < 4; l++) {
+                const unsigned q = (unsigned)(blk[2 + 2 * (4 * ib + l)] | (blk[3 + 2 * (4 * ib + l)] << 8));
+                iq_put8(out + 32 * ib + 8 * l, db[l / 2], qwo_iq_grid(1, (int)(q & 511)), iq_signs7(q >> 9));
+            }
+        }
+    } else if (fmt == QWO_W_IQ2_S) { /* d | qs[32] index low bits | signs[32] | qh[8] (2 high bits each) | scales[8] */
+        for (int ib = 0; ib < 8; ib++) {
+            const uint8_t sc = blk[74 + ib], qh = blk[66 + ib];
+            const float db[2] = {d * (0.5f + (float)(sc & 15)) * 0.25f, d * (0.5f + (float)(sc >> 4)) * 0.25f};
+            for (int l = 0; l < 4; l++) {
+                const int idx = blk[2 + 4 * ib + l] | (((qh >> (2 * l)) & 3) << 8);
+                iq_put8(out + 32 * ib + 8 * l, db[l / 2], qwo_iq_grid(2, idx), blk[34 + 4 * ib + l]);
+            }
+        }
+    } else if (fmt == QWO_W_IQ3_XXS) { /* d | qs[64] grid indices | per 32 weights 4 x 7 sign bits | 4-bit scale */
+        for (int ib = 0; ib < 8; ib++) {
+            const uint8_t* q = blk + 2 + 8 * ib;
+            const uint32_t a = w_u32(blk + 66 + 4 * ib);
+            const float db = d * (0.5f + (float)(a >> 28)) * 0.5f;
+            for (int l = 0; l < 4; l++) {
+                const uint64_t g = qwo_iq_grid(3, q[2 * l]) | (qwo_iq_grid(3, q[2 * l + 1]) << 32);
+                iq_put8(out + 32 * ib + 8 * l, db, g, iq_signs7(a >> (7 * l)));
+            }
+        }
+    } else { /* IQ3_S: d | qs[64] index low bytes | qh[8] (9th bits) | signs[32] | scales[4]: 4-bit per 32 */
+        for (int ib = 0; ib < 8; ib++) {
+            const uint8_t* q = blk + 2 + 8 * ib;
+            const uint8_t qh = blk[66 + ib];
+            const float db = d * (float)(1 + 2 * ((blk[106 + ib / 2] >> (4 * (ib & 1))) & 15));
+            for (int l = 0; l < 4; l++) {
+                const int i0 = q[2 * l] | (((qh >> (2 * l)) & 1) << 8), i1 = q[2 * l + 1] | (((qh >> (2 * l + 1)) & 1) << 8);
+                const uint64_t g = qwo_iq_grid(4, i0) | (qwo_iq_grid(4, i1) << 32);
+                iq_put8(out + 32 * ib + 8 * l, db, g, blk[74 + 4 * ib + l]);
+            }
+        }
     }
 }
 
@@ -588,6 +681,8 @@ int qwo_w_dequant_row(int fmt, const uint8_t* row, float* y, int64_t K) {
                 const int code = (low4 | (high2 << 4)) - 32;
                 out[k] = d * (float)sc[8 * h + 2 * r + l / 16] * (float)code;
             }
+        } else if (fmt != QWO_W_IQ4_XS) {
+            w_dequant_iq(fmt, row + qwo_w_row_bytes(fmt, 256) * b, out);
         } else { /* IQ4_XS: d | scales_h (u16) | scales_l[4] | qs[128]: 8 sub-blocks of 32, 4-bit level indices */
             const uint8_t* blk = row + 136 * b;
             const float d = w_h(blk);

@@ -90,7 +90,13 @@ void qwo_deltanet(const float* qkv, const float* z, const float* b, const float*
 /* Weight formats of the output-projection consumer (decode GEMV over ActQ8 activations, prefill fp16 dequant):
  * ggml block layouts of src/quant/quant_formats.h:92-104, 256 weights per block.  Format ids are the reference's
  * QuantFormat values (include/q38rt/q38rt_types.h:36-66). */
-enum { QWO_W_Q2_K = 10, QWO_W_Q4_K = 12, QWO_W_Q6_K = 14, QWO_W_IQ4_XS = 23, QWO_W_BF16 = 30 };
+enum {
+    QWO_W_Q2_K = 10, QWO_W_Q4_K = 12, QWO_W_Q6_K = 14, QWO_W_IQ2_XXS = 16, QWO_W_IQ2_XS = 17, QWO_W_IQ3_XXS = 18,
+    QWO_W_IQ3_S = 21, QWO_W_IQ2_S = 22, QWO_W_IQ4_XS = 23, QWO_W_BF16 = 30
+};
+/* Entry idx of an i-quant codebook as its little-endian grid bytes (table: 0 IQ2XXS, 1 IQ2XS, 2 IQ2S, 3 IQ3XXS,
+ * 4 IQ3S); 0 for an index out of range. */
+uint64_t qwo_iq_grid(int table, int idx);
 /* bytes of one row of K weights (0 for an unsupported format or K not a multiple of the block) */
 size_t qwo_w_row_bytes(int fmt, int64_t K);
 /* dequantize one row of K weights to fp32; 0 on success, -1 for an unsupported format */

@@ -10,12 +10,19 @@
 // of the group, g / m = the group's scale / min).  Weight bytes stream once through HBM; the activations (a few KB)
 // stay in L1 / L2.  A column's result does not depend on how many columns share the call.
 //
-// Formats (ggml layouts of src/quant/quant_formats.h:92-104): Q2_K, Q4_K, Q6_K, IQ4_XS; BF16 through gemv_bf16 and
-// the dequantizer.  The IQ1 / IQ2 / IQ3 grid formats are not built (their codebooks are not part of this library).
+// Formats (ggml layouts of src/quant/quant_formats.h:92-104): Q2_K, Q4_K, Q6_K, IQ4_XS and the grid formats IQ2_XXS,
+// IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S; BF16 through gemv_bf16 and the dequantizer.  A grid format's codebook is expanded
+// from its code words (iq_grids.inc) into LDS by every workgroup, then each lane looks its grid entries up there; the
+// signs are applied to the int8 codes, so the dot products stay exact v_dot4 integer sums.  IQ1_S / IQ1_M are not
+// built.
 #include "launch.hpp"
 #include "qwattn_common.hpp"
 
 namespace qwa {
+
+#define IQ_TABLE static constexpr
+#include "iq_grids.inc"
+#undef IQ_TABLE
 
 constexpr int GV_WAVES = 8;  // rows (waves) per workgroup
 
@@ -42,10 +49,16 @@ struct WSub {
 
 template <int FMT> struct WFmt;
 
-template <> struct WFmt<QWA_W_Q4_K> {  // d | dmin | scales[12] | qs[128]
+// Formats without a codebook
+struct NoGrid {
+    static constexpr int GRID_DWORDS = 0;
+    __device__ static void fill(uint32_t*, int, int) {}
+};
+
+template <> struct WFmt<QWA_W_Q4_K> : NoGrid {  // d | dmin | scales[12] | qs[128]
     static constexpr int BYTES = 144, BIAS = 0;
     static constexpr bool HALVES = false, MINS = true;
-    __device__ static void sub(const uint8_t* b, int j, WSub& w) {
+    __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t*) {
         const float d = gv_h(b), dmin = gv_h(b + 2);
         const uint32_t s0 = gv_u32(b + 4), s1 = gv_u32(b + 8), s2 = gv_u32(b + 12);
         const uint8_t sc[12] = {(uint8_t)s0, (uint8_t)(s0 >> 8), (uint8_t)(s0 >> 16), (uint8_t)(s0 >> 24),
@@ -70,10 +83,10 @@ template <> struct WFmt<QWA_W_Q4_K> {  // d | dmin | scales[12] | qs[128]
     }
 };
 
-template <> struct WFmt<QWA_W_Q2_K> {  // scales[16] | qs[64] | d | dmin
+template <> struct WFmt<QWA_W_Q2_K> : NoGrid {  // scales[16] | qs[64] | d | dmin
     static constexpr int BYTES = 84, BIAS = 0;
     static constexpr bool HALVES = true, MINS = true;
-    __device__ static void sub(const uint8_t* b, int j, WSub& w) {
+    __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t*) {
         const uint32_t dd = gv_u32(b + 80);
         const float d = h2f_bits((uint16_t)dd), dmin = h2f_bits((uint16_t)(dd >> 16));
         const uint32_t scw = gv_u32(b + 4 * (j >> 1));
@@ -89,10 +102,10 @@ template <> struct WFmt<QWA_W_Q2_K> {  // scales[16] | qs[64] | d | dmin
     }
 };
 
-template <> struct WFmt<QWA_W_Q6_K> {  // ql[128] | qh[64] | scales[16] (int8) | d
+template <> struct WFmt<QWA_W_Q6_K> : NoGrid {  // ql[128] | qh[64] | scales[16] (int8) | d
     static constexpr int BYTES = 210, BIAS = 32;
     static constexpr bool HALVES = true, MINS = false;
-    __device__ static void sub(const uint8_t* b, int j, WSub& w) {
+    __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t*) {
         const int h = j >> 2, r = j & 3;
         const float d = gv_h(b + 208);
         const uint8_t* ql = b + 64 * h + 32 * (r & 1);
@@ -111,7 +124,7 @@ template <> struct WFmt<QWA_W_Q6_K> {  // ql[128] | qh[64] | scales[16] (int8) |
     }
 };
 
-template <> struct WFmt<QWA_W_IQ4_XS> {  // d | scales_h (u16) | scales_l[4] | qs[128]
+template <> struct WFmt<QWA_W_IQ4_XS> : NoGrid {  // d | scales_h (u16) | scales_l[4] | qs[128]
     static constexpr int BYTES = 136, BIAS = 0;
     static constexpr bool HALVES = false, MINS = false;
     // the 16 non-uniform levels as four little-endian dwords (ggml's kvalues_iq4nl, src/quant/iq_tables.inc:373-375)
@@ -122,7 +135,7 @@ template <> struct WFmt<QWA_W_IQ4_XS> {  // d | scales_h (u16) | scales_l[4] | q
         const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
         return (hi & m) | (lo & ~m);
     }
-    __device__ static void sub(const uint8_t* b, int j, WSub& w) {
+    __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t*) {
         const uint32_t hdr = gv_u32(b), sl = gv_u32(b + 4);
         const float d = h2f_bits((uint16_t)hdr);
         const uint32_t shi = hdr >> 16;
@@ -139,6 +152,137 @@ template <> struct WFmt<QWA_W_IQ4_XS> {  // d | scales_h (u16) | scales_l[4] | q
     }
 };
 
+// ---- i-quant grid formats (src/quant/quant_ref.cpp:105-222) ----------------------------------------------------
+// Expands a codebook (entries of NB bytes, each byte LEVELS[index of BITS bits]) into LDS as NB / 4 dwords per entry.
+template <int N, int NB, int BITS>
+__device__ __forceinline__ void iq_fill(uint32_t* lds, const uint16_t* codes, const uint8_t* levels, int t, int nt) {
+    for (int e = t; e < N; e += nt) {
+        const uint32_t c = codes[e];
+#pragma unroll
+        for (int w = 0; w < NB / 4; w++) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) v |= (uint32_t)levels[(c >> (BITS * (4 * w + j))) & ((1u << BITS) - 1)] << (8 * j);
+            lds[e * (NB / 4) + w] = v;
+        }
+    }
+}
+
+// the bytes of g whose sign bit (4 bits, bit j for byte j) is set, negated (g's bytes are 1..127, so no borrow)
+__device__ __forceinline__ uint32_t iq_neg(uint32_t g, uint32_t s4) {
+    const uint32_t one = ((s4 & 15u) * 0x00204081u) & 0x01010101u;
+    return (g ^ (one * 0xFFu)) + one;
+}
+// ggml's ksigns: a 7-bit index plus the parity bit that makes the number of negative signs even
+__device__ __forceinline__ uint32_t iq_signs7(uint32_t s7) {
+    s7 &= 127u;
+    return s7 | ((uint32_t)(__builtin_popcount(s7) & 1) << 7);
+}
+
+template <> struct WFmt<QWA_W_IQ2_XXS> {  // d | per 32 weights: 4 grid indices, then 4 x 7 sign bits | 4-bit scale
+    static constexpr int BYTES = 66, BIAS = 0, GRID_DWORDS = 2 * IQ2XXS_N;
+    static constexpr bool HALVES = false, MINS = false;
+    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ2XXS_N, 8, IQ2XXS_BITS>(lds, IQ2XXS_CODES, IQ2XXS_LEVELS, t, nt); }
+    __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
+        const float d = gv_h(b);
+        const uint32_t a0 = gv_u32_a2(b + 2 + 8 * j), a1 = gv_u32_a2(b + 6 + 8 * j);
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const uint32_t* g = grid + 2 * ((a0 >> (8 * l)) & 255);
+            const uint32_t sg = iq_signs7(a1 >> (7 * l));
+            w.c[2 * l] = iq_neg(g[0], sg);
+            w.c[2 * l + 1] = iq_neg(g[1], sg >> 4);
+        }
+        w.g0 = w.g1 = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
+        w.m0 = w.m1 = 0.0f;
+    }
+};
+
+template <> struct WFmt<QWA_W_IQ2_XS> {  // d | qs[32] u16 (9-bit index | 7 sign bits) | scales[8] (two 4-bit per 32)
+    static constexpr int BYTES = 74, BIAS = 0, GRID_DWORDS = 2 * IQ2XS_N;
+    static constexpr bool HALVES = true, MINS = false;
+    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ2XS_N, 8, IQ2XS_BITS>(lds, IQ2XS_CODES, IQ2XS_LEVELS, t, nt); }
+    __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
+        const float d = gv_h(b);
+        const uint32_t q01 = gv_u32_a2(b + 2 + 8 * j), q23 = gv_u32_a2(b + 6 + 8 * j);
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const uint32_t q = ((l < 2 ? q01 : q23) >> (16 * (l & 1))) & 0xFFFFu;
+            const uint32_t* g = grid + 2 * (q & 511u);
+            const uint32_t sg = iq_signs7(q >> 9);
+            w.c[2 * l] = iq_neg(g[0], sg);
+            w.c[2 * l + 1] = iq_neg(g[1], sg >> 4);
+        }
+        const uint32_t sc = b[66 + j];
+        w.g0 = d * (0.5f + (float)(sc & 15u)) * 0.25f;
+        w.g1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+        w.m0 = w.m1 = 0.0f;
+    }
+};
+
+template <> struct WFmt<QWA_W_IQ2_S> {  // d | qs[32] index low bytes | signs[32] | qh[8] (2 high bits each) | scales[8]
+    static constexpr int BYTES = 82, BIAS = 0, GRID_DWORDS = 2 * IQ2S_N;
+    static constexpr bool HALVES = true, MINS = false;
+    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ2S_N, 8, IQ2S_BITS>(lds, IQ2S_CODES, IQ2S_LEVELS, t, nt); }
+    __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
+        const float d = gv_h(b);
+        const uint32_t lo = gv_u32_a2(b + 2 + 4 * j), sg4 = gv_u32_a2(b + 34 + 4 * j), qh = b[66 + j];
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const uint32_t idx = ((lo >> (8 * l)) & 255u) | (((qh >> (2 * l)) & 3u) << 8);
+            const uint32_t* g = grid + 2 * idx;
+            const uint32_t sg = sg4 >> (8 * l);
+            w.c[2 * l] = iq_neg(g[0], sg);
+            w.c[2 * l + 1] = iq_neg(g[1], sg >> 4);
+        }
+        const uint32_t sc = b[74 + j];
+        w.g0 = d * (0.5f + (float)(sc & 15u)) * 0.25f;
+        w.g1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+        w.m0 = w.m1 = 0.0f;
+    }
+};
+
+template <> struct WFmt<QWA_W_IQ3_XXS> {  // d | qs[64] grid indices | per 32 weights 4 x 7 sign bits | 4-bit scale
+    static constexpr int BYTES = 98, BIAS = 0, GRID_DWORDS = IQ3XXS_N;
+    static constexpr bool HALVES = false, MINS = false;
+    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ3XXS_N, 4, IQ3XXS_BITS>(lds, IQ3XXS_CODES, IQ3XXS_LEVELS, t, nt); }
+    __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
+        const float d = gv_h(b);
+        const uint32_t i0 = gv_u32_a2(b + 2 + 8 * j), i1 = gv_u32_a2(b + 6 + 8 * j), a = gv_u32_a2(b + 66 + 4 * j);
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const uint32_t q = (l < 2 ? i0 : i1) >> (16 * (l & 1));
+            const uint32_t sg = iq_signs7(a >> (7 * l));
+            w.c[2 * l] = iq_neg(grid[q & 255u], sg);
+            w.c[2 * l + 1] = iq_neg(grid[(q >> 8) & 255u], sg >> 4);
+        }
+        w.g0 = w.g1 = d * (0.5f + (float)(a >> 28)) * 0.5f;
+        w.m0 = w.m1 = 0.0f;
+    }
+};
+
+template <> struct WFmt<QWA_W_IQ3_S> {  // d | qs[64] index low bytes | qh[8] (9th bits) | signs[32] | scales[4]
+    static constexpr int BYTES = 110, BIAS = 0, GRID_DWORDS = IQ3S_N;
+    static constexpr bool HALVES = false, MINS = false;
+    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ3S_N, 4, IQ3S_BITS>(lds, IQ3S_CODES, IQ3S_LEVELS, t, nt); }
+    __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
+        const float d = gv_h(b);
+        const uint32_t i0 = gv_u32_a2(b + 2 + 8 * j), i1 = gv_u32_a2(b + 6 + 8 * j), qh = b[66 + j];
+        const uint32_t sg4 = gv_u32_a2(b + 74 + 4 * j);
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const uint32_t q = (l < 2 ? i0 : i1) >> (16 * (l & 1));
+            const uint32_t ia = (q & 255u) | (((qh >> (2 * l)) & 1u) << 8);
+            const uint32_t ib = ((q >> 8) & 255u) | (((qh >> (2 * l + 1)) & 1u) << 8);
+            const uint32_t sg = sg4 >> (8 * l);
+            w.c[2 * l] = iq_neg(grid[ia], sg);
+            w.c[2 * l + 1] = iq_neg(grid[ib], sg >> 4);
+        }
+        w.g0 = w.g1 = d * (float)(1 + 2 * (int)((b[106 + j / 2] >> (4 * (j & 1))) & 15));
+        w.m0 = w.m1 = 0.0f;
+    }
+};
+
 // One wave per row; NB activation columns at aq + c * act_ld (d / s at + c * act_ld / 32)
 template <int FMT, int NB>
 __global__ void __launch_bounds__(GV_WAVES * 64) k_gemv_q8(const uint8_t* __restrict__ W, size_t row_bytes, int K,
@@ -150,6 +294,11 @@ __global__ void __launch_bounds__(GV_WAVES * 64) k_gemv_q8(const uint8_t* __rest
     const int lane = threadIdx.x & 63;
     const int nsub = K / 32;
     const uint32_t ones = 0x01010101u;
+    __shared__ uint32_t s_grid[F::GRID_DWORDS > 0 ? F::GRID_DWORDS : 1];
+    if constexpr (F::GRID_DWORDS > 0) {
+        F::fill(s_grid, threadIdx.x, GV_WAVES * 64);
+        __syncthreads();
+    }
     for (int row = blockIdx.x * GV_WAVES + (int)(threadIdx.x >> 6); row < N; row += gridDim.x * GV_WAVES) {
         const uint8_t* wr = W + (size_t)row * row_bytes;
         float acc[NB];
@@ -157,7 +306,7 @@ __global__ void __launch_bounds__(GV_WAVES * 64) k_gemv_q8(const uint8_t* __rest
         for (int c = 0; c < NB; c++) acc[c] = 0.0f;
         for (int u = lane; u < nsub; u += 64) {
             WSub w;
-            F::sub(wr + (size_t)(u >> 3) * F::BYTES, u & 7, w);
+            F::sub(wr + (size_t)(u >> 3) * F::BYTES, u & 7, w, s_grid);
 #pragma unroll
             for (int c = 0; c < NB; c++) {
                 const uint4* xp = reinterpret_cast<const uint4*>(aq + (size_t)c * act_ld + 32 * u);
@@ -166,15 +315,19 @@ __global__ void __launch_bounds__(GV_WAVES * 64) k_gemv_q8(const uint8_t* __rest
                 int i0 = dot4(w.c[0], x0.x, dot4(w.c[1], x0.y, dot4(w.c[2], x0.z, dot4(w.c[3], x0.w, 0))));
                 int i1 = dot4(w.c[4], x1.x, dot4(w.c[5], x1.y, dot4(w.c[6], x1.z, dot4(w.c[7], x1.w, 0))));
                 if constexpr (F::HALVES) {
-                    const int q0 = dot4(ones, x0.x, dot4(ones, x0.y, dot4(ones, x0.z, dot4(ones, x0.w, 0))));
-                    const int q1 = dot4(ones, x1.x, dot4(ones, x1.y, dot4(ones, x1.z, dot4(ones, x1.w, 0))));
-                    if constexpr (F::BIAS != 0) {
-                        i0 -= F::BIAS * q0;
-                        i1 -= F::BIAS * q1;
+                    if constexpr (F::BIAS != 0 || F::MINS) {
+                        const int q0 = dot4(ones, x0.x, dot4(ones, x0.y, dot4(ones, x0.z, dot4(ones, x0.w, 0))));
+                        const int q1 = dot4(ones, x1.x, dot4(ones, x1.y, dot4(ones, x1.z, dot4(ones, x1.w, 0))));
+                        if constexpr (F::BIAS != 0) {
+                            i0 -= F::BIAS * q0;
+                            i1 -= F::BIAS * q1;
+                        }
+                        float v = w.g0 * (float)i0 + w.g1 * (float)i1;
+                        if constexpr (F::MINS) v -= w.m0 * (float)q0 + w.m1 * (float)q1;
+                        acc[c] = fmaf(dx, v, acc[c]);
+                    } else {
+                        acc[c] = fmaf(dx, w.g0 * (float)i0 + w.g1 * (float)i1, acc[c]);
                     }
-                    float v = w.g0 * (float)i0 + w.g1 * (float)i1;
-                    if constexpr (F::MINS) v -= w.m0 * (float)q0 + w.m1 * (float)q1;
-                    acc[c] = fmaf(dx, v, acc[c]);
                 } else {
                     acc[c] = fmaf(dx * w.g0, (float)(i0 + i1), acc[c]);
                     if constexpr (F::MINS) acc[c] = fmaf(-w.m0, as[(size_t)c * (act_ld / 32) + u], acc[c]);
@@ -238,16 +391,16 @@ __global__ void __launch_bounds__(256) k_gemv_bf16(const uint16_t* __restrict__ 
 // no FMA contraction.
 #pragma clang fp contract(off)
 template <int FMT>
-__device__ __forceinline__ void dq_sub(const uint8_t* b, int j, float* v) {
+__device__ __forceinline__ void dq_sub(const uint8_t* b, int j, float* v, const uint32_t* grid) {
     if constexpr (FMT == QWA_W_Q4_K) {
         WSub w;
-        WFmt<FMT>::sub(b, j, w);
+        WFmt<FMT>::sub(b, j, w, grid);
         // w.g0 = d * s6, w.m0 = dmin * m6, as the reference's d1 / m1
 #pragma unroll
         for (int i = 0; i < 32; i++) v[i] = w.g0 * (float)((w.c[i / 4] >> (8 * (i % 4))) & 0xFF) - w.m0;
     } else if constexpr (FMT == QWA_W_Q2_K) {
         WSub w;
-        WFmt<FMT>::sub(b, j, w);
+        WFmt<FMT>::sub(b, j, w, grid);
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             const float code = (float)((w.c[i / 4] >> (8 * (i % 4))) & 0xFF);
@@ -255,17 +408,17 @@ __device__ __forceinline__ void dq_sub(const uint8_t* b, int j, float* v) {
         }
     } else if constexpr (FMT == QWA_W_Q6_K) {
         WSub w;
-        WFmt<FMT>::sub(b, j, w);
+        WFmt<FMT>::sub(b, j, w, grid);
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             const float code = (float)((int)((w.c[i / 4] >> (8 * (i % 4))) & 0xFF) - 32);
             v[i] = (i < 16 ? w.g0 : w.g1) * code;
         }
-    } else {  // IQ4_XS
+    } else {  // IQ4_XS and the grid formats: signed int8 codes times the sub-block's (half) scale
         WSub w;
-        WFmt<FMT>::sub(b, j, w);
+        WFmt<FMT>::sub(b, j, w, grid);
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = w.g0 * (float)(int8_t)((w.c[i / 4] >> (8 * (i % 4))) & 0xFF);
+        for (int i = 0; i < 32; i++) v[i] = (i < 16 ? w.g0 : w.g1) * (float)(int8_t)((w.c[i / 4] >> (8 * (i % 4))) & 0xFF);
     }
 }
 
@@ -273,11 +426,16 @@ template <int FMT>
 __global__ void __launch_bounds__(256) k_dequant_f16(const uint8_t* __restrict__ W, size_t row_bytes, int K, int rows,
                                                      uint16_t* __restrict__ out) {
     const int nsub = K / 32;
+    __shared__ uint32_t s_grid[WFmt<FMT>::GRID_DWORDS > 0 ? WFmt<FMT>::GRID_DWORDS : 1];
+    if constexpr (WFmt<FMT>::GRID_DWORDS > 0) {
+        WFmt<FMT>::fill(s_grid, threadIdx.x, 256);
+        __syncthreads();
+    }
     const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
     if (i >= (long long)rows * nsub) return;
     const int r = (int)(i / nsub), u = (int)(i % nsub);
     float v[32];
-    dq_sub<FMT>(W + (size_t)r * row_bytes + (size_t)(u >> 3) * WFmt<FMT>::BYTES, u & 7, v);
+    dq_sub<FMT>(W + (size_t)r * row_bytes + (size_t)(u >> 3) * WFmt<FMT>::BYTES, u & 7, v, s_grid);
     // the fp32 values stay opaque to the conversion: otherwise a product and its fp16 rounding fold into one
     // mixed-precision fma with a +0 addend, which turns -0 into +0
 #pragma unroll
@@ -306,12 +464,18 @@ size_t w_row_bytes(int fmt, long long K) {
         case QWA_W_Q4_K: return (size_t)(K / 256) * WFmt<QWA_W_Q4_K>::BYTES;
         case QWA_W_Q6_K: return (size_t)(K / 256) * WFmt<QWA_W_Q6_K>::BYTES;
         case QWA_W_IQ4_XS: return (size_t)(K / 256) * WFmt<QWA_W_IQ4_XS>::BYTES;
+        case QWA_W_IQ2_XXS: return (size_t)(K / 256) * WFmt<QWA_W_IQ2_XXS>::BYTES;
+        case QWA_W_IQ2_XS: return (size_t)(K / 256) * WFmt<QWA_W_IQ2_XS>::BYTES;
+        case QWA_W_IQ2_S: return (size_t)(K / 256) * WFmt<QWA_W_IQ2_S>::BYTES;
+        case QWA_W_IQ3_XXS: return (size_t)(K / 256) * WFmt<QWA_W_IQ3_XXS>::BYTES;
+        case QWA_W_IQ3_S: return (size_t)(K / 256) * WFmt<QWA_W_IQ3_S>::BYTES;
         default: return 0;
     }
 }
 
 bool gemv_q8_supported(int fmt) {
-    return fmt == QWA_W_Q2_K || fmt == QWA_W_Q4_K || fmt == QWA_W_Q6_K || fmt == QWA_W_IQ4_XS;
+    return fmt == QWA_W_Q2_K || fmt == QWA_W_Q4_K || fmt == QWA_W_Q6_K || fmt == QWA_W_IQ4_XS || fmt == QWA_W_IQ2_XXS ||
+           fmt == QWA_W_IQ2_XS || fmt == QWA_W_IQ2_S || fmt == QWA_W_IQ3_XXS || fmt == QWA_W_IQ3_S;
 }
 
 template <int FMT>
@@ -335,6 +499,11 @@ hipError_t launch_gemv_q8(int fmt, const void* W, size_t rb, int K, int N, const
         case QWA_W_Q4_K: return gemv_fmt<QWA_W_Q4_K>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
         case QWA_W_Q6_K: return gemv_fmt<QWA_W_Q6_K>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
         case QWA_W_IQ4_XS: return gemv_fmt<QWA_W_IQ4_XS>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
+        case QWA_W_IQ2_XXS: return gemv_fmt<QWA_W_IQ2_XXS>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
+        case QWA_W_IQ2_XS: return gemv_fmt<QWA_W_IQ2_XS>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
+        case QWA_W_IQ2_S: return gemv_fmt<QWA_W_IQ2_S>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
+        case QWA_W_IQ3_XXS: return gemv_fmt<QWA_W_IQ3_XXS>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
+        case QWA_W_IQ3_S: return gemv_fmt<QWA_W_IQ3_S>(W, rb, K, N, a, nb, act_ld, y, y_ld, accumulate, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -366,6 +535,11 @@ hipError_t launch_dequant_f16(int fmt, const void* W, size_t rb, int K, int rows
         case QWA_W_Q4_K: hipLaunchKernelGGL(k_dequant_f16<QWA_W_Q4_K>, grid, block, 0, st, w, rb, K, rows, out); break;
         case QWA_W_Q6_K: hipLaunchKernelGGL(k_dequant_f16<QWA_W_Q6_K>, grid, block, 0, st, w, rb, K, rows, out); break;
         case QWA_W_IQ4_XS: hipLaunchKernelGGL(k_dequant_f16<QWA_W_IQ4_XS>, grid, block, 0, st, w, rb, K, rows, out); break;
+        case QWA_W_IQ2_XXS: hipLaunchKernelGGL(k_dequant_f16<QWA_W_IQ2_XXS>, grid, block, 0, st, w, rb, K, rows, out); break;
+        case QWA_W_IQ2_XS: hipLaunchKernelGGL(k_dequant_f16<QWA_W_IQ2_XS>, grid, block, 0, st, w, rb, K, rows, out); break;
+        case QWA_W_IQ2_S: hipLaunchKernelGGL(k_dequant_f16<QWA_W_IQ2_S>, grid, block, 0, st, w, rb, K, rows, out); break;
+        case QWA_W_IQ3_XXS: hipLaunchKernelGGL(k_dequant_f16<QWA_W_IQ3_XXS>, grid, block, 0, st, w, rb, K, rows, out); break;
+        case QWA_W_IQ3_S: hipLaunchKernelGGL(k_dequant_f16<QWA_W_IQ3_S>, grid, block, 0, st, w, rb, K, rows, out); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -488,6 +488,7 @@ def deltanet_rows(p: DNParams, qkv, z, beta_raw, alpha_raw, B: int, cin: int, ep
 
 # ---- consumers of the attention output (src/cuda/gemv.cuh:20-39, src/cuda/prefill.cuh:16-18) ------------------------
 W_Q2_K, W_Q4_K, W_Q6_K, W_IQ4_XS, W_BF16 = 10, 12, 14, 23, 30
+W_IQ2_XXS, W_IQ2_XS, W_IQ3_XXS, W_IQ3_S, W_IQ2_S = 16, 17, 18, 21, 22
 
 
 def w_row_bytes(fmt: int, K: int) -> int:

@@ -123,8 +123,9 @@ int main() {
                hipStream_t) = deltanet_multi;
     void (*dr)(const DeltaNetParams&, const float*, const float*, const float*, const float*, int, int, float, void*,
                float*, __half*, hipStream_t) = deltanet_rows;
-    enum class QuantFormat : uint32_t { Q4_K = 12, IQ3_S = 21 };
-    if (!gemv_q8_supported(QuantFormat::Q4_K) || gemv_q8_supported(QuantFormat::IQ3_S)) return 5;
+    enum class QuantFormat : uint32_t { Q4_K = 12, IQ1_S = 19, IQ3_S = 21 };
+    if (!gemv_q8_supported(QuantFormat::Q4_K) || !gemv_q8_supported(QuantFormat::IQ3_S) ||
+        gemv_q8_supported(QuantFormat::IQ1_S)) return 5;
     bool (*gq)(QuantFormat, const void*, size_t, int, int, const ActQ8&, float*, hipStream_t, bool) = gemv_q8;
     bool (*gn)(QuantFormat, const void*, size_t, int, int, const ActQ8&, int, int, float*, int, hipStream_t, bool) =
         gemv_q8n;

@@ -6,7 +6,8 @@ oracle, with the reference's own criteria (tests/kernels/test_gemv.cu:69-121):
 - the activation quantizer bit-exact.
 
 Also: every column of the multi-column GEMV bit-identical to the single-column call, the accumulate flag, the BF16
-GEMV, and rejected formats.  Weights are random bytes in each format (no model file ships here)."""
+GEMV, and rejected formats.  Weights are random bytes in each format (no model file ships here); the grid formats
+IQ2_XXS / IQ2_XS / IQ2_S / IQ3_XXS / IQ3_S are those of the model's attention output projection."""
 import numpy as np
 import pytest
 import torch
@@ -16,8 +17,11 @@ from wutil import random_rows
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [ops.W_Q2_K, ops.W_Q4_K, ops.W_Q6_K, ops.W_IQ4_XS]
-NAMES = {ops.W_Q2_K: "q2_k", ops.W_Q4_K: "q4_k", ops.W_Q6_K: "q6_k", ops.W_IQ4_XS: "iq4_xs", ops.W_BF16: "bf16"}
+FMTS = [ops.W_Q2_K, ops.W_Q4_K, ops.W_Q6_K, ops.W_IQ4_XS, ops.W_IQ2_XXS, ops.W_IQ2_XS, ops.W_IQ2_S, ops.W_IQ3_XXS,
+        ops.W_IQ3_S]
+NAMES = {ops.W_Q2_K: "q2_k", ops.W_Q4_K: "q4_k", ops.W_Q6_K: "q6_k", ops.W_IQ4_XS: "iq4_xs", ops.W_BF16: "bf16",
+         ops.W_IQ2_XXS: "iq2_xxs", ops.W_IQ2_XS: "iq2_xs", ops.W_IQ2_S: "iq2_s", ops.W_IQ3_XXS: "iq3_xxs",
+         ops.W_IQ3_S: "iq3_s"}
 
 
 def act(x):
@@ -128,7 +132,7 @@ def test_rejected_formats(gpu):
     W = torch.zeros(4096, dtype=torch.uint8, device="cuda")
     a = ops.ActQ8.allocate(256)
     y = torch.empty(4, device="cuda")
-    for fmt in (21, 16, 0):  # IQ3_S, IQ2_XXS (grid formats), FP32
+    for fmt in (19, 29, 0):  # IQ1_S, IQ1_M (grid formats without a kernel), FP32
         assert not ops.gemv_q8_supported(fmt)
         with pytest.raises(ops.QwaError):
             ops.gemv_q8(fmt, W, 1024, 256, 4, a, y)

@@ -4,7 +4,8 @@ import numpy as np
 import oracle as O
 
 # byte offsets of the fp16 scale fields inside one 256-weight block
-SCALE_OFFSETS = {O.W_Q4_K: [0, 2], O.W_Q2_K: [80, 82], O.W_Q6_K: [208], O.W_IQ4_XS: [0]}
+SCALE_OFFSETS = {O.W_Q4_K: [0, 2], O.W_Q2_K: [80, 82], O.W_Q6_K: [208], O.W_IQ4_XS: [0], O.W_IQ2_XXS: [0],
+                 O.W_IQ2_XS: [0], O.W_IQ2_S: [0], O.W_IQ3_XXS: [0], O.W_IQ3_S: [0]}
 
 
 def random_rows(fmt, N, K, seed, scale=0.01):
