@@ -30,6 +30,19 @@
 
 namespace qwa {
 
+#ifdef QWA_TRACE
+// experimental phase stamps (trace builds only): [workgroup][8] realtime-clock values written by wave 0, lane 0
+static __device__ unsigned long long dec_trace[4096][8];
+#define TRACE(k)                                                                                         \
+    do {                                                                                                 \
+        if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][k] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define TRACE(k) \
+    do {         \
+    } while (0)
+#endif
+
 constexpr int REC = 260;    // partial record: m, l, 2 pad, O[256] (16-byte aligned O)
 constexpr int CGRP = 16;    // combine: records per fixed summation group
 constexpr int CHUNK = 16;   // keys per chunk
@@ -260,11 +273,22 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;  // chunks of this wave
     const size_t rowbase = (size_t)g * kv.capacity;
 
+    TRACE(0);
+    uint8_t(*ring)[C::BYTES] = s_u.ring[wave];
+    auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * min(j, nmine - 1)); };
+    auto issue = [&](uint8_t* dst, int kb) { issue_chunk<KVT>(dst, kv, rowbase, kb, kmax, lane); };
+    // the ring's loads go out before the Q set-up, so their HBM latency overlaps it
+    if (nmine > 0) {
+#pragma unroll
+        for (int st = 0; st < NST; st++) issue(ring[st], chunk_key(st));
+    }
+
     // Q / 16 as fp16 hi + lo parts, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + perm(j);
     // the fragments are loaded once per workgroup through LDS
     __shared__ __attribute__((aligned(16))) h8 s_q[RT * 8 * 2 * 64];
     q_frags_to_lds<KVT, RT>(q, nq, g, rt0, s_q);
     __syncthreads();
+    TRACE(1);
     h8 qh[RT][8], ql[RT][8];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
@@ -292,16 +316,12 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     }
 
     if (nmine > 0) {
-        uint8_t(*ring)[C::BYTES] = s_u.ring[wave];
-        auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * min(j, nmine - 1)); };
-        auto issue = [&](uint8_t* dst, int kb) { issue_chunk<KVT>(dst, kv, rowbase, kb, kmax, lane); };
-#pragma unroll
-        for (int st = 0; st < NST; st++) issue(ring[st], chunk_key(st));
         for (int j = 0; j < nmine; j++) {
             const int slot = j % NST;
             const int kb = chunk_key(j);
             wait_vmcnt<C::NLOAD * (NST - 1)>();  // this slot has landed; the later ones may still fly
             __builtin_amdgcn_wave_barrier();
+            if (j == 0) TRACE(2);
             const uint8_t* kst = ring[slot];
             const uint8_t* vst = kst + C::KBYTES;
             const uint16_t* ksc = reinterpret_cast<const uint16_t*>(kst + 2 * C::KBYTES);
@@ -400,6 +420,7 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
         }
         wait_vmcnt<0>();  // drain the clamped prefetches before the ring is reused or the wave exits
     }
+    TRACE(3);
 
     // ---- merge the 4 classes as fold(fold(c0, c1), fold(c2, c3)) per row tile; wave 0 writes the records
 #pragma unroll
@@ -426,6 +447,7 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
             }
         }
     }
+    TRACE(4);
     prof_end(prof);
 }
 
@@ -969,6 +991,14 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
                        oq != nullptr ? 1 : 0);
     return hipGetLastError();
 }
+
+#ifdef QWA_TRACE
+}  // namespace qwa
+extern "C" int qwa_trace_read(unsigned long long* host, int nwg) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(qwa::dec_trace), sizeof(unsigned long long) * 8 * nwg);
+}
+namespace qwa {
+#endif
 
 // ---- allocation-free decode: the partial records live in a file-scope device array instead of a work argument.
 // Its size is dec_work_bytes() (25.6 MB), which covers every valid call (up to 8 queries, any context up to
