@@ -223,3 +223,20 @@ def test_decode_in_hip_graph(gpu):
         assert torch.equal(out, want), rep
         assert torch.equal(_decode(kv, q, gate, n - 5, nq), _decode(kv, q, gate, n - 5, nq))
     del g
+
+
+@pytest.mark.parametrize("kvt,nq", [(ops.Q4_0, 8), (ops.F16, 1), (ops.Q8_0, 3)],
+                         ids=["q4_0-nq8", "f16-nq1", "q8_0-nq3"])
+def test_decode_at_max_positions(gpu, oracle, kvt, nq):
+    """The largest context the path supports (attn_max_positions = 262144; src/cuda/ops.cu:1002-1008): the last
+    queries end exactly at position 262143, every record of the split is in use, against the oracle."""
+    n = ops.attn_max_positions()
+    print(f"decode at max positions kvt={KV_NAMES[kvt]} nq={nq}", flush=True)
+    kv, _, _ = make_cache(kvt, n, n, seed=70 + kvt)
+    q, gate = _qg(nq, 71 + nq)
+    out = _decode(kv, q, gate, n - nq, nq)
+    Kd, Vd = dequant_cache(kv, n)
+    ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, n - nq, nq)
+    assert_close(out.cpu().numpy(), ref, f"decode {KV_NAMES[kvt]} at {n} positions")
+    with pytest.raises(ops.QwaError, match="262144"):
+        _decode(kv, q, gate, n - nq + 1, nq)

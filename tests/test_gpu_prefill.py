@@ -185,3 +185,24 @@ def test_prefill_two_streams_do_not_interfere(gpu):
             assert np.array_equal(o.float().cpu().numpy(), w), f"rep {rep}"
     for s in streams:
         ops.attn_prefill_release(stream=s)
+
+
+def test_prefill_at_max_positions(gpu, oracle):
+    """A 1024-token chunk ending at the largest supported position (262144), with a caller-owned workspace sized
+    for it; a sample of 24 queries (every 43rd token plus the last) against the oracle."""
+    kvt, n, B = ops.Q4_0, ops.attn_max_positions(), 1024
+    p0 = n - B
+    kv, _, _ = make_cache(kvt, n, n, seed=81)
+    q = seeded_normal((B, 24, 256), 182).half().float()
+    gate = seeded_normal((B, 24, 256), 183)
+    work = torch.empty(ops.attn_prefill_work_bytes(B, n), dtype=torch.uint8, device="cuda")
+    out = torch.empty((B, 24, 256), dtype=torch.float16, device="cuda")
+    ops.attn_prefill_ws(q, gate, kv, kvt, B, p0, out, work)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    del work
+    Kd, Vd = dequant_cache(kv, n)
+    ts = list(range(0, B, 43)) + [B - 1]
+    qn, gn = q.cpu().numpy(), gate.cpu().numpy()
+    refs = np.stack([oracle.attention(qn[t:t + 1], gn[t:t + 1], Kd, Vd, p0 + t, 1)[0] for t in ts])
+    assert_close(got[ts], refs, "prefill ending at 262144")
