@@ -39,6 +39,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--positions", type=int, default=150000)
+    ap.add_argument("--nq", type=int, default=1,
+                    help="queries per headline call (7: the speculative-verify variant of the same workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="headline decode only")
     ap.add_argument("--consumer-only", action="store_true",
@@ -122,7 +124,7 @@ def main():
     work = torch.empty(ops.attn_work_bytes(n) // 4 + 1, dtype=torch.float32, device="cuda")
     out = torch.empty((8, 24, 256), device="cuda")
 
-    def step(nq=1):
+    def step(nq=args.nq):
         for kv in layers:
             ops.attn_decode_multi(q, gate, kv, kvt, n - nq, nq, work, out)
 
@@ -144,8 +146,10 @@ def main():
     for _ in range(args.steps):
         step()
     kern_ms, kern_n = ops.profile_end()
-    kern_us = kern_ms * 1000.0 / max(kern_n, 1)
-    kern_dev_us = ops.profile_device_ms() * 1000.0 / max(kern_n, 1)
+    # per call (a 7-query verify is two launches: the split-K passes over row tiles 0-1 and tile 2)
+    calls = args.steps * L
+    kern_us = kern_ms * 1000.0 / calls
+    kern_dev_us = ops.profile_device_ms() * 1000.0 / calls
     us_layer = ms_per_step * 1000.0 / L
     if args.copy_probe:
         src = torch.empty(1 << 27, dtype=torch.float32, device="cuda").fill_(1.0)
@@ -170,17 +174,18 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (K/V ~N(0,1), 1% of key rows x8, quantized on append; random gate logits)",
-        "config": {"workload": "decode_q4_0_150k", "kv": "q4_0", "positions": n, "queries_per_call": 1,
+        "config": {"workload": "decode_q4_0_150k" if args.nq == 1 else f"verify{args.nq}_q4_0_150k", "kv": "q4_0",
+                   "positions": n, "queries_per_call": args.nq,
                    "layers_per_step": L, "q_heads": 24, "kv_heads": 4, "head_dim": 256},
         "decode_us_per_layer": round(us_layer, 3),
         "roofline": {"bound": "hbm", "achieved": round(bytes_layer / (kern_us * 1e-6) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(bytes_layer / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": KDEC_TRAFFIC if (n, L) == (150000, 16) else None,
+                     "traffic": KDEC_TRAFFIC if (n, L, args.nq) == (150000, 16, 1) else None,
                      "traffic_source": "rocprofv3 --pmc FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), calibrated on a "
                                        "512 MiB copy, per k_dec4 dispatch",
-                     "kernel": "k_dec4 (split-K Q4_0 decode), average over the timed launches",
-                     "kernel_us": round(kern_us, 3), "launches": kern_n,
+                     "kernel": "k_dec4 (split-K Q4_0 decode), kernel time per call averaged over the timed calls",
+                     "kernel_us": round(kern_us, 3), "launches": kern_n, "calls": calls,
                      "kernel_us_device_clock": round(kern_dev_us, 3),
                      "algorithmic_bytes_per_launch": bytes_layer},
     }
