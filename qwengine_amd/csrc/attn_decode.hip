@@ -619,6 +619,7 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
         if (kb + CHUNK - 1 <= kmax) q4_issue_full(dst, kv, rowbase + kb, off, lane);
         else q4_issue_tail(dst, kv, rowbase, kb, kmax, lane);
     };
+    TRACE(0);
     // the first chunk's loads go out before the Q set-up, so their latency overlaps it; the rest of the ring follows
     // the set-up, so the first iteration waits for chunk 0 only
     if (nmine > 0) issue(0);
@@ -776,8 +777,14 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
             // software-pipelined: iteration j multiplies chunk j's V while it scores chunk j + 1, so the two chunks'
             // MFMA and VALU chains interleave within the wave.  Per row the operations and their order are those of
             // one chunk after the other: the P.V of chunk j, then the softmax of chunk j + 1, whose rescale covers it.
+#ifdef QWA_TRACE
+            unsigned long long wsum = 0, tw = __builtin_amdgcn_s_memtime();
+            const unsigned long long tloop = tw;
+#endif
+            TRACE(1);
             if (NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
             else wait_vmcnt<0>();
+            TRACE(2);
             h4 P[1];
             VRegs vr;
             {
@@ -791,8 +798,15 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
                 if (NST < nmine) issue(NST);
             }
             for (int j = 0; j + 1 < nmine; j++) {
+#ifdef QWA_TRACE
+                tw = __builtin_amdgcn_s_memtime();
+#endif
                 if (j + 1 + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();
                 else wait_vmcnt<0>();
+#ifdef QWA_TRACE
+                __builtin_amdgcn_s_waitcnt(0);
+                wsum += __builtin_amdgcn_s_memtime() - tw;
+#endif
                 KRegs kr;
                 read_k(j + 1, kr);
                 f4 S[1];
@@ -805,6 +819,12 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
                 P[0] = Pn;
             }
             pv(vr, P);
+            TRACE(3);
+#ifdef QWA_TRACE
+            if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][5] = wsum;
+            if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][6] = nmine;
+            if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][7] = __builtin_amdgcn_s_memtime() - tloop;
+#endif
         } else {
             for (int j = 0; j < nmine; j++) {
                 if (j + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
@@ -851,6 +871,7 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
             }
         }
     }
+    TRACE(4);
     prof_end(prof);
 }
 
