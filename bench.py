@@ -330,11 +330,13 @@ def consumer_extras(ops, torch, steps):
         blocks[:, :, 1] = 0x1c  # every d (and Q4_K's dmin) field a small fp16 value: bytes xx 1c ~ 0.004
         if fmt == ops.W_Q4_K:
             blocks[:, :, 3] = 0x1c
-        W = [torch.from_numpy(Wn).cuda() for _ in range(4)]  # 4 copies: 71 MB, more than one XCD's caches
+        # enough copies to pass 300 MB, so that neither the L2s nor the 256 MB MALL serve the weights
+        nw = -(-300_000_000 // (N * rb))
+        W = [torch.from_numpy(Wn).cuda() for _ in range(nw)]
 
         def run():
             for i in range(16):
-                ops.gemv_q8(fmt, W[i % 4], rb, K, N, a, y)
+                ops.gemv_q8(fmt, W[i % nw], rb, K, N, a, y)
         ms = time_graph(torch, run, max(5, steps // 5))
         us = ms * 1000.0 / 16
         out[f"gemv_{name}_6144x5120_us"] = round(us, 3)

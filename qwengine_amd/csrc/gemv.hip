@@ -60,18 +60,14 @@ template <> struct WFmt<QWA_W_Q4_K> : NoGrid {  // d | dmin | scales[12] | qs[12
     static constexpr bool HALVES = false, MINS = true;
     __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t*) {
         const float d = gv_h(b), dmin = gv_h(b + 2);
+        // 6-bit scale / min of sub-block j from the 12 scale bytes, by shifts (a byte array indexed by the lane's j
+        // would compile to compare / select chains): j < 4 takes the low 6 bits of bytes j and j + 4; j >= 4 the
+        // nibbles of byte j + 4 and the top 2 bits of bytes j - 4 and j
         const uint32_t s0 = gv_u32(b + 4), s1 = gv_u32(b + 8), s2 = gv_u32(b + 12);
-        const uint8_t sc[12] = {(uint8_t)s0, (uint8_t)(s0 >> 8), (uint8_t)(s0 >> 16), (uint8_t)(s0 >> 24),
-                                (uint8_t)s1, (uint8_t)(s1 >> 8), (uint8_t)(s1 >> 16), (uint8_t)(s1 >> 24),
-                                (uint8_t)s2, (uint8_t)(s2 >> 8), (uint8_t)(s2 >> 16), (uint8_t)(s2 >> 24)};
-        int s6, m6;
-        if (j < 4) {
-            s6 = sc[j] & 63;
-            m6 = sc[j + 4] & 63;
-        } else {
-            s6 = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4);
-            m6 = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
-        }
+        const uint32_t sh8 = 8 * (j & 3), b0 = s0 >> sh8, b1 = s1 >> sh8, b2 = s2 >> sh8;
+        const uint32_t lo = 0u - (uint32_t)(j < 4);  // all ones for j < 4: a mask select, no branch between loads
+        const int s6 = (int)(((b0 & 63u) & lo) | (((b2 & 15u) | ((b0 >> 2) & 0x30u)) & ~lo));
+        const int m6 = (int)(((b1 & 63u) & lo) | ((((b2 >> 4) & 15u) | ((b1 >> 2) & 0x30u)) & ~lo));
         const uint4* q = reinterpret_cast<const uint4*>(b + 16 + 32 * (j >> 1));
         const uint4 a = q[0], bb = q[1];
         const uint32_t raw[8] = {a.x, a.y, a.z, a.w, bb.x, bb.y, bb.z, bb.w};
@@ -283,8 +279,16 @@ template <> struct WFmt<QWA_W_IQ3_S> {  // d | qs[64] index low bytes | qh[8] (9
     }
 };
 
+#ifndef QWA_GV_BATCH
+#define QWA_GV_BATCH -1  // -1: per format as below; 0 / 1: never / always (tuning builds)
+#endif
+template <int FMT> struct GvBatched {
+    static constexpr bool value =
+        QWA_GV_BATCH >= 0 ? QWA_GV_BATCH == 1 : FMT != QWA_W_IQ4_XS && FMT != QWA_W_Q2_K && FMT != QWA_W_Q6_K;
+};
+
 // One wave per row; NB activation columns at aq + c * act_ld (d / s at + c * act_ld / 32)
-template <int FMT, int NB>
+template <int FMT, int NB, int U>
 __global__ void __launch_bounds__(GV_WAVES * 64) k_gemv_q8(const uint8_t* __restrict__ W, size_t row_bytes, int K,
                                                            int N, const int8_t* __restrict__ aq,
                                                            const float* __restrict__ ad, const float* __restrict__ as,
@@ -304,33 +308,55 @@ __global__ void __launch_bounds__(GV_WAVES * 64) k_gemv_q8(const uint8_t* __rest
         float acc[NB];
 #pragma unroll
         for (int c = 0; c < NB; c++) acc[c] = 0.0f;
-        for (int u = lane; u < nsub; u += 64) {
-            WSub w;
-            F::sub(wr + (size_t)(u >> 3) * F::BYTES, u & 7, w, s_grid);
+        // U sub-blocks per lane at a time: every weight and activation load of the batch (and, for the grid formats,
+        // the codebook reads that depend on them) is issued before any of them is used.  Indices past the row are
+        // clamped so that the batch stays one basic block, and their products are dropped by a select.  Sub-blocks
+        // are accumulated in the order u = lane, lane + 64, ... whatever U is.
+        for (int u0 = lane; u0 < nsub; u0 += 64 * U) {
+            WSub w[U];
+            uint4 x0[U][NB], x1[U][NB];
+            float dx[U][NB], sx[U][NB];
 #pragma unroll
-            for (int c = 0; c < NB; c++) {
-                const uint4* xp = reinterpret_cast<const uint4*>(aq + (size_t)c * act_ld + 32 * u);
-                const uint4 x0 = xp[0], x1 = xp[1];
-                const float dx = ad[(size_t)c * (act_ld / 32) + u];
-                int i0 = dot4(w.c[0], x0.x, dot4(w.c[1], x0.y, dot4(w.c[2], x0.z, dot4(w.c[3], x0.w, 0))));
-                int i1 = dot4(w.c[4], x1.x, dot4(w.c[5], x1.y, dot4(w.c[6], x1.z, dot4(w.c[7], x1.w, 0))));
-                if constexpr (F::HALVES) {
-                    if constexpr (F::BIAS != 0 || F::MINS) {
-                        const int q0 = dot4(ones, x0.x, dot4(ones, x0.y, dot4(ones, x0.z, dot4(ones, x0.w, 0))));
-                        const int q1 = dot4(ones, x1.x, dot4(ones, x1.y, dot4(ones, x1.z, dot4(ones, x1.w, 0))));
-                        if constexpr (F::BIAS != 0) {
-                            i0 -= F::BIAS * q0;
-                            i1 -= F::BIAS * q1;
+            for (int k = 0; k < U; k++) {
+                const int u = min(u0 + 64 * k, nsub - 1);
+                F::sub(wr + (size_t)(u >> 3) * F::BYTES, u & 7, w[k], s_grid);
+#pragma unroll
+                for (int c = 0; c < NB; c++) {
+                    const uint4* xp = reinterpret_cast<const uint4*>(aq + (size_t)c * act_ld + 32 * u);
+                    x0[k][c] = xp[0];
+                    x1[k][c] = xp[1];
+                    dx[k][c] = ad[(size_t)c * (act_ld / 32) + u];
+                    sx[k][c] = (!F::HALVES && F::MINS) ? as[(size_t)c * (act_ld / 32) + u] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < U; k++) {
+                const bool valid = u0 + 64 * k < nsub;
+#pragma unroll
+                for (int c = 0; c < NB; c++) {
+                    const float acc_in = acc[c];
+                    const uint4 xa = x0[k][c], xb = x1[k][c];
+                    int i0 = dot4(w[k].c[0], xa.x, dot4(w[k].c[1], xa.y, dot4(w[k].c[2], xa.z, dot4(w[k].c[3], xa.w, 0))));
+                    int i1 = dot4(w[k].c[4], xb.x, dot4(w[k].c[5], xb.y, dot4(w[k].c[6], xb.z, dot4(w[k].c[7], xb.w, 0))));
+                    if constexpr (F::HALVES) {
+                        if constexpr (F::BIAS != 0 || F::MINS) {
+                            const int q0 = dot4(ones, xa.x, dot4(ones, xa.y, dot4(ones, xa.z, dot4(ones, xa.w, 0))));
+                            const int q1 = dot4(ones, xb.x, dot4(ones, xb.y, dot4(ones, xb.z, dot4(ones, xb.w, 0))));
+                            if constexpr (F::BIAS != 0) {
+                                i0 -= F::BIAS * q0;
+                                i1 -= F::BIAS * q1;
+                            }
+                            float v = w[k].g0 * (float)i0 + w[k].g1 * (float)i1;
+                            if constexpr (F::MINS) v -= w[k].m0 * (float)q0 + w[k].m1 * (float)q1;
+                            acc[c] = fmaf(dx[k][c], v, acc[c]);
+                        } else {
+                            acc[c] = fmaf(dx[k][c], w[k].g0 * (float)i0 + w[k].g1 * (float)i1, acc[c]);
                         }
-                        float v = w.g0 * (float)i0 + w.g1 * (float)i1;
-                        if constexpr (F::MINS) v -= w.m0 * (float)q0 + w.m1 * (float)q1;
-                        acc[c] = fmaf(dx, v, acc[c]);
                     } else {
-                        acc[c] = fmaf(dx, w.g0 * (float)i0 + w.g1 * (float)i1, acc[c]);
+                        acc[c] = fmaf(dx[k][c] * w[k].g0, (float)(i0 + i1), acc[c]);
+                        if constexpr (F::MINS) acc[c] = fmaf(-w[k].m0, sx[k][c], acc[c]);
                     }
-                } else {
-                    acc[c] = fmaf(dx * w.g0, (float)(i0 + i1), acc[c]);
-                    if constexpr (F::MINS) acc[c] = fmaf(-w.m0, as[(size_t)c * (act_ld / 32) + u], acc[c]);
+                    acc[c] = valid ? acc[c] : acc_in;
                 }
             }
         }
@@ -483,12 +509,27 @@ static hipError_t gemv_fmt(const void* W, size_t rb, int K, int N, const qwa_act
                            int y_ld, int acc, hipStream_t st) {
     const dim3 grid((unsigned)min((N + GV_WAVES - 1) / GV_WAVES, 65535)), block(GV_WAVES * 64);
     const uint8_t* w = static_cast<const uint8_t*>(W);
+    // one column: a lane's sub-block rounds (K / 2048 of them, up to 4) loaded as one batch, for the formats whose
+    // decode chain is long enough to gain from it (measured: Q4_K and the grid formats; IQ4_XS, Q2_K, Q6_K run
+    // faster one sub-block at a time).  Several columns keep one sub-block per batch (registers).
+    const int rounds = (K / 32 + 63) / 64;
+    const int ub = (nb == 1 && GvBatched<FMT>::value) ? min(rounds, 4) : 1;
+#define QWA_GV_LAUNCH(NB, U) \
+    hipLaunchKernelGGL((k_gemv_q8<FMT, NB, U>), grid, block, 0, st, w, rb, K, N, a.q, a.d, a.s, act_ld, y, y_ld, acc)
     switch (nb) {
-        case 1: hipLaunchKernelGGL((k_gemv_q8<FMT, 1>), grid, block, 0, st, w, rb, K, N, a.q, a.d, a.s, act_ld, y, y_ld, acc); break;
-        case 2: hipLaunchKernelGGL((k_gemv_q8<FMT, 2>), grid, block, 0, st, w, rb, K, N, a.q, a.d, a.s, act_ld, y, y_ld, acc); break;
-        case 3: hipLaunchKernelGGL((k_gemv_q8<FMT, 3>), grid, block, 0, st, w, rb, K, N, a.q, a.d, a.s, act_ld, y, y_ld, acc); break;
-        default: hipLaunchKernelGGL((k_gemv_q8<FMT, 4>), grid, block, 0, st, w, rb, K, N, a.q, a.d, a.s, act_ld, y, y_ld, acc); break;
+        case 1:
+            switch (ub) {
+                case 1: QWA_GV_LAUNCH(1, 1); break;
+                case 2: QWA_GV_LAUNCH(1, 2); break;
+                case 3: QWA_GV_LAUNCH(1, 3); break;
+                default: QWA_GV_LAUNCH(1, 4); break;
+            }
+            break;
+        case 2: QWA_GV_LAUNCH(2, 1); break;
+        case 3: QWA_GV_LAUNCH(3, 1); break;
+        default: QWA_GV_LAUNCH(4, 1); break;
     }
+#undef QWA_GV_LAUNCH
     return hipGetLastError();
 }
 
