@@ -13,8 +13,13 @@
 // Formats (ggml layouts of src/quant/quant_formats.h:92-104): Q2_K, Q4_K, Q6_K, IQ4_XS and the grid formats IQ2_XXS,
 // IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S; BF16 through gemv_bf16 and the dequantizer.  A grid format's codebook is expanded
 // from its code words (iq_grids.inc) into LDS by every workgroup, then each lane looks its grid entries up there; the
-// signs are applied to the int8 codes, so the dot products stay exact v_dot4 integer sums.  IQ1_S / IQ1_M are not
-// built.
+// signs are applied to the int8 codes (through a table of byte masks, also in LDS, for all but IQ3_S), so the dot
+// products stay exact v_dot4 integer sums.  IQ1_S / IQ1_M are not built.
+//
+// What bounds it: a graph-replayed launch costs ~2.6 us even when empty, and beyond that the kernel is VALU-bound
+// (the decode of a sub-block costs more issue cycles than its bytes take to arrive).  The decode therefore avoids
+// runtime-indexed byte arrays (compare / select chains), branches between loads (a second round trip) and integer
+// multiplies where a table or a shift does.
 #include "launch.hpp"
 #include "qwattn_common.hpp"
 
@@ -150,19 +155,28 @@ template <> struct WFmt<QWA_W_IQ4_XS> : NoGrid {  // d | scales_h (u16) | scales
 
 // ---- i-quant grid formats (src/quant/quant_ref.cpp:105-222) ----------------------------------------------------
 // Expands a codebook (entries of NB bytes, each byte LEVELS[index of BITS bits]) into LDS as NB / 4 dwords per entry.
-template <int N, int NB, int BITS>
-__device__ __forceinline__ void iq_fill(uint32_t* lds, const uint16_t* codes, const uint8_t* levels, int t, int nt) {
+// The (at most 8) levels travel as two packed dwords, so a byte is one v_perm lookup, not a dependent memory read.
+constexpr uint32_t iq_pack(const uint8_t* lv, int n, int o) {
+    uint32_t v = 0;
+    for (int j = 0; j < 4; j++) v |= o + j < n ? (uint32_t)lv[o + j] << (8 * j) : 0u;
+    return v;
+}
+template <int N, int NB, int BITS, uint32_t LV_LO, uint32_t LV_HI>
+__device__ __forceinline__ void iq_fill(uint32_t* lds, const uint16_t* codes, int t, int nt) {
     for (int e = t; e < N; e += nt) {
         const uint32_t c = codes[e];
 #pragma unroll
         for (int w = 0; w < NB / 4; w++) {
-            uint32_t v = 0;
+            uint32_t sel = 0;
 #pragma unroll
-            for (int j = 0; j < 4; j++) v |= (uint32_t)levels[(c >> (BITS * (4 * w + j))) & ((1u << BITS) - 1)] << (8 * j);
-            lds[e * (NB / 4) + w] = v;
+            for (int j = 0; j < 4; j++) sel |= ((c >> (BITS * (4 * w + j))) & ((1u << BITS) - 1)) << (8 * j);
+            lds[e * (NB / 4) + w] = __builtin_amdgcn_perm(LV_HI, LV_LO, sel);
         }
     }
 }
+#define QWA_IQ_FILL(P, NB) \
+    iq_fill<P##_N, NB, P##_BITS, iq_pack(P##_LEVELS, sizeof(P##_LEVELS), 0), iq_pack(P##_LEVELS, sizeof(P##_LEVELS), 4)>( \
+        lds, P##_CODES, t, nt)
 
 // the bytes of g whose sign bit (4 bits, bit j for byte j) is set, negated (g's bytes are 1..127, so no borrow)
 __device__ __forceinline__ uint32_t iq_neg(uint32_t g, uint32_t s4) {
@@ -175,19 +189,42 @@ __device__ __forceinline__ uint32_t iq_signs7(uint32_t s7) {
     return s7 | ((uint32_t)(__builtin_popcount(s7) & 1) << 7);
 }
 
+// Sign masks in LDS, after each grid format's codebook: entry e < 256 holds, for the sign byte e, two dwords whose
+// byte k is 0xFF where bit k of e is set; entry 256 + i the same for ggml's ksigns of the 7-bit index i.  Applying
+// one is an xor and an add per 4 weights (iq_apply), instead of spreading the bits with integer multiplies.
+constexpr int IQ_SIGN_DWORDS = 2 * (256 + 128);
+__device__ __forceinline__ void iq_fill_signs(uint32_t* t, int tid, int nt) {
+    for (int e = tid; e < 256 + 128; e += nt) {
+        const uint32_t sg = e < 256 ? (uint32_t)e : iq_signs7((uint32_t)(e - 256));
+        uint32_t m0 = 0, m1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            m0 |= ((sg >> k) & 1u) * (0xFFu << (8 * k));
+            m1 |= ((sg >> (k + 4)) & 1u) * (0xFFu << (8 * k));
+        }
+        t[2 * e] = m0;
+        t[2 * e + 1] = m1;
+    }
+}
+// the bytes of g under the 0xFF bytes of mask m, negated (g's bytes are 1..127, so no borrow crosses a byte)
+__device__ __forceinline__ uint32_t iq_apply(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
+
 template <> struct WFmt<QWA_W_IQ2_XXS> {  // d | per 32 weights: 4 grid indices, then 4 x 7 sign bits | 4-bit scale
-    static constexpr int BYTES = 66, BIAS = 0, GRID_DWORDS = 2 * IQ2XXS_N;
+    static constexpr int BYTES = 66, BIAS = 0, CODE_DWORDS = 2 * IQ2XXS_N, GRID_DWORDS = CODE_DWORDS + IQ_SIGN_DWORDS;
     static constexpr bool HALVES = false, MINS = false;
-    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ2XXS_N, 8, IQ2XXS_BITS>(lds, IQ2XXS_CODES, IQ2XXS_LEVELS, t, nt); }
+    __device__ static void fill(uint32_t* lds, int t, int nt) {
+        QWA_IQ_FILL(IQ2XXS, 8);
+        iq_fill_signs(lds + CODE_DWORDS, t, nt);
+    }
     __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
         const float d = gv_h(b);
         const uint32_t a0 = gv_u32_a2(b + 2 + 8 * j), a1 = gv_u32_a2(b + 6 + 8 * j);
 #pragma unroll
         for (int l = 0; l < 4; l++) {
             const uint32_t* g = grid + 2 * ((a0 >> (8 * l)) & 255);
-            const uint32_t sg = iq_signs7(a1 >> (7 * l));
-            w.c[2 * l] = iq_neg(g[0], sg);
-            w.c[2 * l + 1] = iq_neg(g[1], sg >> 4);
+            const uint32_t* m = grid + CODE_DWORDS + 2 * (256 + ((a1 >> (7 * l)) & 127));
+            w.c[2 * l] = iq_apply(g[0], m[0]);
+            w.c[2 * l + 1] = iq_apply(g[1], m[1]);
         }
         w.g0 = w.g1 = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
         w.m0 = w.m1 = 0.0f;
@@ -195,9 +232,12 @@ template <> struct WFmt<QWA_W_IQ2_XXS> {  // d | per 32 weights: 4 grid indices,
 };
 
 template <> struct WFmt<QWA_W_IQ2_XS> {  // d | qs[32] u16 (9-bit index | 7 sign bits) | scales[8] (two 4-bit per 32)
-    static constexpr int BYTES = 74, BIAS = 0, GRID_DWORDS = 2 * IQ2XS_N;
+    static constexpr int BYTES = 74, BIAS = 0, CODE_DWORDS = 2 * IQ2XS_N, GRID_DWORDS = CODE_DWORDS + IQ_SIGN_DWORDS;
     static constexpr bool HALVES = true, MINS = false;
-    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ2XS_N, 8, IQ2XS_BITS>(lds, IQ2XS_CODES, IQ2XS_LEVELS, t, nt); }
+    __device__ static void fill(uint32_t* lds, int t, int nt) {
+        QWA_IQ_FILL(IQ2XS, 8);
+        iq_fill_signs(lds + CODE_DWORDS, t, nt);
+    }
     __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
         const float d = gv_h(b);
         const uint32_t q01 = gv_u32_a2(b + 2 + 8 * j), q23 = gv_u32_a2(b + 6 + 8 * j);
@@ -205,9 +245,9 @@ template <> struct WFmt<QWA_W_IQ2_XS> {  // d | qs[32] u16 (9-bit index | 7 sign
         for (int l = 0; l < 4; l++) {
             const uint32_t q = ((l < 2 ? q01 : q23) >> (16 * (l & 1))) & 0xFFFFu;
             const uint32_t* g = grid + 2 * (q & 511u);
-            const uint32_t sg = iq_signs7(q >> 9);
-            w.c[2 * l] = iq_neg(g[0], sg);
-            w.c[2 * l + 1] = iq_neg(g[1], sg >> 4);
+            const uint32_t* m = grid + CODE_DWORDS + 2 * (256 + (q >> 9));
+            w.c[2 * l] = iq_apply(g[0], m[0]);
+            w.c[2 * l + 1] = iq_apply(g[1], m[1]);
         }
         const uint32_t sc = b[66 + j];
         w.g0 = d * (0.5f + (float)(sc & 15u)) * 0.25f;
@@ -217,9 +257,12 @@ template <> struct WFmt<QWA_W_IQ2_XS> {  // d | qs[32] u16 (9-bit index | 7 sign
 };
 
 template <> struct WFmt<QWA_W_IQ2_S> {  // d | qs[32] index low bytes | signs[32] | qh[8] (2 high bits each) | scales[8]
-    static constexpr int BYTES = 82, BIAS = 0, GRID_DWORDS = 2 * IQ2S_N;
+    static constexpr int BYTES = 82, BIAS = 0, CODE_DWORDS = 2 * IQ2S_N, GRID_DWORDS = CODE_DWORDS + IQ_SIGN_DWORDS;
     static constexpr bool HALVES = true, MINS = false;
-    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ2S_N, 8, IQ2S_BITS>(lds, IQ2S_CODES, IQ2S_LEVELS, t, nt); }
+    __device__ static void fill(uint32_t* lds, int t, int nt) {
+        QWA_IQ_FILL(IQ2S, 8);
+        iq_fill_signs(lds + CODE_DWORDS, t, nt);
+    }
     __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
         const float d = gv_h(b);
         const uint32_t lo = gv_u32_a2(b + 2 + 4 * j), sg4 = gv_u32_a2(b + 34 + 4 * j), qh = b[66 + j];
@@ -227,9 +270,9 @@ template <> struct WFmt<QWA_W_IQ2_S> {  // d | qs[32] index low bytes | signs[32
         for (int l = 0; l < 4; l++) {
             const uint32_t idx = ((lo >> (8 * l)) & 255u) | (((qh >> (2 * l)) & 3u) << 8);
             const uint32_t* g = grid + 2 * idx;
-            const uint32_t sg = sg4 >> (8 * l);
-            w.c[2 * l] = iq_neg(g[0], sg);
-            w.c[2 * l + 1] = iq_neg(g[1], sg >> 4);
+            const uint32_t* m = grid + CODE_DWORDS + 2 * ((sg4 >> (8 * l)) & 255u);
+            w.c[2 * l] = iq_apply(g[0], m[0]);
+            w.c[2 * l + 1] = iq_apply(g[1], m[1]);
         }
         const uint32_t sc = b[74 + j];
         w.g0 = d * (0.5f + (float)(sc & 15u)) * 0.25f;
@@ -239,18 +282,21 @@ template <> struct WFmt<QWA_W_IQ2_S> {  // d | qs[32] index low bytes | signs[32
 };
 
 template <> struct WFmt<QWA_W_IQ3_XXS> {  // d | qs[64] grid indices | per 32 weights 4 x 7 sign bits | 4-bit scale
-    static constexpr int BYTES = 98, BIAS = 0, GRID_DWORDS = IQ3XXS_N;
+    static constexpr int BYTES = 98, BIAS = 0, CODE_DWORDS = IQ3XXS_N, GRID_DWORDS = CODE_DWORDS + IQ_SIGN_DWORDS;
     static constexpr bool HALVES = false, MINS = false;
-    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ3XXS_N, 4, IQ3XXS_BITS>(lds, IQ3XXS_CODES, IQ3XXS_LEVELS, t, nt); }
+    __device__ static void fill(uint32_t* lds, int t, int nt) {
+        QWA_IQ_FILL(IQ3XXS, 4);
+        iq_fill_signs(lds + CODE_DWORDS, t, nt);
+    }
     __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
         const float d = gv_h(b);
         const uint32_t i0 = gv_u32_a2(b + 2 + 8 * j), i1 = gv_u32_a2(b + 6 + 8 * j), a = gv_u32_a2(b + 66 + 4 * j);
 #pragma unroll
         for (int l = 0; l < 4; l++) {
             const uint32_t q = (l < 2 ? i0 : i1) >> (16 * (l & 1));
-            const uint32_t sg = iq_signs7(a >> (7 * l));
-            w.c[2 * l] = iq_neg(grid[q & 255u], sg);
-            w.c[2 * l + 1] = iq_neg(grid[(q >> 8) & 255u], sg >> 4);
+            const uint32_t* m = grid + CODE_DWORDS + 2 * (256 + ((a >> (7 * l)) & 127u));
+            w.c[2 * l] = iq_apply(grid[q & 255u], m[0]);
+            w.c[2 * l + 1] = iq_apply(grid[(q >> 8) & 255u], m[1]);
         }
         w.g0 = w.g1 = d * (0.5f + (float)(a >> 28)) * 0.5f;
         w.m0 = w.m1 = 0.0f;
@@ -258,9 +304,11 @@ template <> struct WFmt<QWA_W_IQ3_XXS> {  // d | qs[64] grid indices | per 32 we
 };
 
 template <> struct WFmt<QWA_W_IQ3_S> {  // d | qs[64] index low bytes | qh[8] (9th bits) | signs[32] | scales[4]
+    // signs spread by multiplies here: with 12 LDS reads per sub-block (8 codebook dwords + 4 mask pairs) the mask
+    // table measured slower than the arithmetic for this format
     static constexpr int BYTES = 110, BIAS = 0, GRID_DWORDS = IQ3S_N;
     static constexpr bool HALVES = false, MINS = false;
-    __device__ static void fill(uint32_t* lds, int t, int nt) { iq_fill<IQ3S_N, 4, IQ3S_BITS>(lds, IQ3S_CODES, IQ3S_LEVELS, t, nt); }
+    __device__ static void fill(uint32_t* lds, int t, int nt) { QWA_IQ_FILL(IQ3S, 4); }
     __device__ static void sub(const uint8_t* b, int j, WSub& w, const uint32_t* grid) {
         const float d = gv_h(b);
         const uint32_t i0 = gv_u32_a2(b + 2 + 8 * j), i1 = gv_u32_a2(b + 6 + 8 * j), qh = b[66 + j];
