@@ -350,6 +350,11 @@ def consumer_extras(ops, torch, steps):
     ms = time_calls(torch, lambda: g.f16(Wh, N, K, Xh, K, B, Y, N), max(10, steps // 2), 3)
     out["gemm_f16_1024x5120x6144_ms"] = round(ms, 4)
     out["gemm_f16_tflops"] = round(2.0 * B * N * K / (ms * 1e-3) / 1e12, 1)
+    # the same shape after qwa_gemm_tune (set-up time measurement of hipBLASLt's candidates)
+    g.tune(Wh, N, K, Xh, K, B, Y, N, max_candidates=32)
+    ms = time_calls(torch, lambda: g.f16(Wh, N, K, Xh, K, B, Y, N), max(10, steps // 2), 3)
+    out["gemm_f16_tuned_1024x5120x6144_ms"] = round(ms, 4)
+    out["gemm_f16_tuned_tflops"] = round(2.0 * B * N * K / (ms * 1e-3) / 1e12, 1)
     g.close()
     return out
 

@@ -279,6 +279,12 @@ int qwa_gemm_bind(void* handle, void* stream, void* workspace, size_t bytes);
 void qwa_gemm_destroy(void* handle);
 int qwa_gemm_f16(void* handle, const uint16_t* W, int N, int K, const uint16_t* X, int ldx, int B, float* Y, int ldy,
                  int accumulate, void* stream);
+/* Set-up companion of qwa_gemm_f16 (no reference counterpart: cuBLAS picks its own kernel): times up to
+ * max_candidates (<= 64; < 1 means 16) of hipBLASLt's algorithms for this shape on the caller's buffers (Y is
+ * overwritten) and keeps the fastest for later qwa_gemm_f16 calls of the shape.  Synchronises the stream; refused
+ * (QWA_ERR_INVALID) while the stream is capturing.  best_us (may be NULL) receives the winner's time per call. */
+int qwa_gemm_tune(void* handle, const uint16_t* W, int N, int K, const uint16_t* X, int ldx, int B, float* Y, int ldy,
+                  int max_candidates, void* stream, float* best_us);
 
 /* Opt-in kernel timing (no reference counterpart; the reference times phases with env-gated GPU timers,
  * src/runtime/engine.cpp:2477-2480): between qwa_profile_begin() and qwa_profile_end(), every launch of an

@@ -115,6 +115,9 @@ EXPORTS = {
     "qwa_gemm_f16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_void_p]),
+    "qwa_gemm_tune": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]),
     "qwa_gemv_q8_supported": (ctypes.c_int, [ctypes.c_int]),
     "qwa_quantize_act_q8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_ActQ8C),
                                            ctypes.c_void_p]),
@@ -540,6 +543,15 @@ class Gemm:
     def f16(self, W, N: int, K: int, X, ldx: int, B: int, Y, ldy: int, accumulate=False, stream=None) -> None:
         _check(lib().qwa_gemm_f16(self.h, _ptr(W), N, K, _ptr(X), ldx, B, _ptr(Y), ldy, 1 if accumulate else 0,
                                   _stream(stream)))
+
+    def tune(self, W, N: int, K: int, X, ldx: int, B: int, Y, ldy: int, max_candidates: int = 16,
+             stream=None) -> float:
+        """Times hipBLASLt's first candidates for this shape (Y is overwritten) and keeps the fastest; returns its
+        time per call in microseconds.  Set-up only: refused while the stream captures."""
+        best = ctypes.c_float(0.0)
+        _check(lib().qwa_gemm_tune(self.h, _ptr(W), N, K, _ptr(X), ldx, B, _ptr(Y), ldy, max_candidates,
+                                   _stream(stream), ctypes.byref(best)))
+        return best.value
 
     def close(self) -> None:
         if self.h:

@@ -163,3 +163,27 @@ def test_gemm_f16_vs_float64(gpu, N, K, B, ldx, ldy):
     assert ((Y[:, :N].double() - 2 * ref).abs() / mag).max().item() < 2e-5
     assert torch.allclose(Y[:, :N], 2 * Y0[:, :N], rtol=1e-6, atol=1e-6)
     g.close()
+
+
+def test_gemm_tune_keeps_a_correct_algorithm(gpu):
+    """qwa_gemm_tune times hipBLASLt's candidates for a shape and keeps the fastest: later calls of the shape stay
+    within the same float64 bound, and tuning is refused while the stream is capturing."""
+    N, K, B = 640, 1024, 96
+    g = ops.Gemm()
+    W = (torch.randn((N, K), device="cuda") * 0.05).half()
+    X = torch.randn((B, K), device="cuda").half()
+    Y = torch.empty((B, N), device="cuda")
+    us = g.tune(W, N, K, X, K, B, Y, N, max_candidates=8)
+    assert us > 0.0
+    Y.fill_(float("nan"))
+    g.f16(W, N, K, X, K, B, Y, N)
+    torch.cuda.synchronize()
+    Xd, Wd = X.double(), W.double()
+    assert ((Y.double() - Xd @ Wd.T).abs() / (Xd.abs() @ Wd.abs().T)).max().item() < 1e-5
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        with pytest.raises(ops.QwaError):
+            g.tune(W, N, K, X, K, B, Y, N, stream=s)
+    g.close()
+
