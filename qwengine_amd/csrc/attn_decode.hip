@@ -15,9 +15,10 @@
 //    online softmax is lane-local up to a 4-lane max / sum, and P^T is directly the B operand of
 //    O^T += V^T P^T (v_mfma_f32_16x16x16_f16, fp32 accumulation; for Q4_0 the V operand holds the exact codes and
 //    the keys' block scales multiply the P operand, one product per block instead of one per V element);
-//  * the 4 classes of a workgroup are merged as fold(fold(c0, c1), fold(c2, c3)) into one partial record
-//    (m, l, O[256]) per row; k_dec_combine merges the records in a fixed order, normalises, applies the sigmoid gate
-//    and the optional ActQ8 epilogue.
+//  * the 8 classes of a workgroup are merged along a fixed pairwise tree into one partial record (m, l, O[256]) per
+//    row; k_dec_combine merges the records in a fixed order, normalises, applies the sigmoid gate and the optional
+//    ActQ8 epilogue;
+//  * a call with several row tiles (verify) streams the cache once per pair of tiles.
 // Every reduction runs over a partition of the keys that depends only on key indices, and masked keys contribute
 // exact zeros, so a query's output does not depend on how many queries share the call (the reference's
 // decode == decode_batch contract, src/cuda/ops.cuh:134-135).
@@ -46,7 +47,7 @@ static __device__ unsigned long long dec_trace[4096][8];
 constexpr int REC = 260;    // partial record: m, l, 2 pad, O[256] (16-byte aligned O)
 constexpr int CGRP = 16;    // combine: records per fixed summation group
 constexpr int CHUNK = 16;   // keys per chunk
-constexpr int WG_CLASSES = 4;
+constexpr int WG_CLASSES = 8;                   // classes (waves) per decode workgroup, every format
 constexpr int NREC = DEC_CLASSES / WG_CLASSES;  // records (workgroups) per KV head
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maximum (natural-log units)
@@ -167,49 +168,50 @@ __device__ __forceinline__ void fold(float& m, float& l, f4* o, float m2, float 
     m = M;
 }
 
-// LDS of the cross-wave merge (aliases the chunk rings once streaming is over)
-struct MergeLds {
-    f4 o[2][16][64];
-    float ml[2][2][64];
-};
-
-// Merges the partial states (m, l, O) of the 4 waves of a workgroup as fold(fold(c0, c1), fold(c2, c3)); returns
-// true in wave 0, which then holds the merged state.  Every wave must call it (it synchronises the workgroup).
-__device__ __forceinline__ bool merge4(MergeLds& s, int wave, int lane, float& m, float& l, f4* o) {
-    __syncthreads();  // every wave is done with the ring (or with the previous merge)
-    if (wave & 1) {
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++) s.o[wave >> 1][dt][lane] = o[dt];
-        s.ml[wave >> 1][0][lane] = m;
-        s.ml[wave >> 1][1][lane] = l;
-    }
-    __syncthreads();
-    if (!(wave & 1)) {
-        f4 o2[16];
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++) o2[dt] = s.o[wave >> 1][dt][lane];
-        fold(m, l, o, s.ml[wave >> 1][0][lane], s.ml[wave >> 1][1][lane], o2);
-    }
-    __syncthreads();
-    if (wave == 2) {
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++) s.o[0][dt][lane] = o[dt];
-        s.ml[0][0][lane] = m;
-        s.ml[0][1][lane] = l;
-    }
-    __syncthreads();
-    if (wave != 0) return false;
-    f4 o2[16];
-#pragma unroll
-    for (int dt = 0; dt < 16; dt++) o2[dt] = s.o[0][dt][lane];
-    fold(m, l, o, s.ml[0][0][lane], s.ml[0][1][lane], o2);
-    return true;
-}
-
 // sum over the 4 lanes l % 16 + 16 k that hold one row
 __device__ __forceinline__ float half4_sum(float x) {
     x += __shfl_xor(x, 16, 64);
     return x + __shfl_xor(x, 32, 64);
+}
+
+// Merge of the partial states of the WGW waves of a workgroup, split across the waves by head dims: every wave puts
+// its state in LDS, then wave w folds the WGW states of the output tiles TPW w .. TPW w + TPW - 1 (TPW = 16 / WGW)
+// in the fixed tree fold(fold(c0, c1), fold(c2, c3)) (and fold(that, the same over c4..c7) for 8 waves).  Every
+// wave folds (m, l) along the same tree, so all of them hold the merged m and l.
+template <int WGW>
+struct MergeLdsN {
+    f4 o[WGW][16][64];
+    float ml[WGW][2][64];
+};
+
+template <int WGW>
+__device__ __forceinline__ void merge_split(MergeLdsN<WGW>& s, int wave, int lane, float& m, float& l, const f4* o,
+                                            f4* om) {
+    constexpr int TPW = 16 / WGW;
+    __syncthreads();  // every wave is done with the ring (or with the previous tile's merge)
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++) s.o[wave][dt][lane] = o[dt];
+    s.ml[wave][0][lane] = m;
+    s.ml[wave][1][lane] = l;
+    __syncthreads();
+    float mm[WGW], ll[WGW];
+    f4 oo[WGW][TPW];
+#pragma unroll
+    for (int w = 0; w < WGW; w++) {
+        mm[w] = s.ml[w][0][lane];
+        ll[w] = s.ml[w][1][lane];
+#pragma unroll
+        for (int t = 0; t < TPW; t++) oo[w][t] = s.o[w][TPW * wave + t][lane];
+    }
+    // pairwise tree: level k folds state i with state i + 2^k into state i
+#pragma unroll
+    for (int step = 1; step < WGW; step *= 2)
+#pragma unroll
+        for (int w = 0; w < WGW; w += 2 * step) fold<TPW>(mm[w], ll[w], oo[w], mm[w + step], ll[w + step], oo[w + step]);
+    m = mm[0];
+    l = ll[0];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) om[t] = oo[0][t];
 }
 
 // Q / 16 as fp16 hi + lo MFMA B-operand fragments of RT row tiles, written to LDS by the whole workgroup:
@@ -245,36 +247,42 @@ __device__ __forceinline__ void q_frags_to_lds(const float* __restrict__ q, int 
     }
 }
 
-// ring depth (chunks in flight per wave): sized so that two 4-wave workgroups fit a CU's 160 KB of LDS where possible
+// ring depth (chunks in flight per wave), sized so that one 8-wave workgroup fits a CU's 160 KB of LDS
 template <int KVT, int RT> struct DecCfg {
     static constexpr int NST = KVT == QWA_KV_Q4_0 ? (RT == 1 ? 3 : 2) : 1;
 };
 
 // RT row tiles starting at tile rt0 (calls with more tiles launch several passes; a row's arithmetic is the same
-// in every pass and every grouping).
-template <int KVT, int RT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// in every pass and every grouping), WGW waves (classes) per workgroup.  RT = 1 keeps Q in registers; RT = 2 reads
+// the Q fragments of both tiles from LDS at use (two tiles of Q and O would not fit two waves per SIMD), so each
+// chunk is streamed and unpacked once for both tiles.
+template <int KVT, int RT, int WGW>
+__global__ void __launch_bounds__(64 * WGW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
       unsigned long long* prof) {
     prof_start(prof);
     using C = ChunkLds<KVT>;
     constexpr int NST = DecCfg<KVT, RT>::NST;
-    // the chunk ring of every wave while streaming; two partial states while merging
+    constexpr bool QLDS = RT > 1;
+    // the Q fragments and the chunk ring of every wave while streaming; the partial states while merging
     __shared__ __attribute__((aligned(16))) union {
-        uint8_t ring[WG_CLASSES][NST][C::BYTES];
-        MergeLds merge;
+        struct {
+            h8 q[RT * 8 * 2 * 64];  // [rt][block][hi, lo][lane]
+            uint8_t ring[WGW][NST][C::BYTES];
+        } a;
+        MergeLdsN<WGW> merge;
     } s_u;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
     const int g = blockIdx.y, rec = blockIdx.x;
     const int kmax = pos0 + nq - 1;
     const int nchunk = kmax / CHUNK + 1;
-    const int cls = rec * WG_CLASSES + wave;
+    const int cls = rec * WGW + wave;
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;  // chunks of this wave
     const size_t rowbase = (size_t)g * kv.capacity;
 
     TRACE(0);
-    uint8_t(*ring)[C::BYTES] = s_u.ring[wave];
+    uint8_t(*ring)[C::BYTES] = s_u.a.ring[wave];
     auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * min(j, nmine - 1)); };
     auto issue = [&](uint8_t* dst, int kb) { issue_chunk<KVT>(dst, kv, rowbase, kb, kmax, lane); };
     // the ring's loads go out before the Q set-up, so their HBM latency overlaps it
@@ -285,18 +293,18 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
 
     // Q / 16 as fp16 hi + lo parts, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + perm(j);
     // the fragments are loaded once per workgroup through LDS
-    __shared__ __attribute__((aligned(16))) h8 s_q[RT * 8 * 2 * 64];
+    h8* s_q = s_u.a.q;
     q_frags_to_lds<KVT, RT>(q, nq, g, rt0, s_q);
     __syncthreads();
     TRACE(1);
-    h8 qh[RT][8], ql[RT][8];
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++)
+    h8 qh[QLDS ? 1 : RT][8], ql[QLDS ? 1 : RT][8];
+    if constexpr (!QLDS) {
 #pragma unroll
         for (int b = 0; b < 8; b++) {
-            qh[rt][b] = s_q[((rt * 8 + b) * 2 + 0) * 64 + lane];
-            ql[rt][b] = s_q[((rt * 8 + b) * 2 + 1) * 64 + lane];
+            qh[0][b] = s_q[(b * 2 + 0) * 64 + lane];
+            ql[0][b] = s_q[(b * 2 + 1) * 64 + lane];
         }
+    }
 
     // rows of this lane (S^T layout, column i16): query qt, head hh, last visible key qpos (-1: padding row)
     int qpos[RT];
@@ -344,8 +352,10 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
                 const h8 ka = k_block_int<KVT>(kst, i16, lg, b);
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
-                    f4 a = mfma16(ka, qh[rt][b], f4{0.0f, 0.0f, 0.0f, 0.0f});
-                    a = mfma16(ka, ql[rt][b], a);
+                    const h8 bh = QLDS ? s_q[((rt * 8 + b) * 2 + 0) * 64 + lane] : qh[QLDS ? 0 : rt][b];
+                    const h8 bl = QLDS ? s_q[((rt * 8 + b) * 2 + 1) * 64 + lane] : ql[QLDS ? 0 : rt][b];
+                    f4 a = mfma16(ka, bh, f4{0.0f, 0.0f, 0.0f, 0.0f});
+                    a = mfma16(ka, bl, a);
                     if constexpr (KVT == QWA_KV_F16) {
                         S[rt] += a;
                     } else {
@@ -422,27 +432,31 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     }
     TRACE(3);
 
-    // ---- merge the 4 classes as fold(fold(c0, c1), fold(c2, c3)) per row tile; wave 0 writes the records
+    // ---- merge the WGW classes of each row tile, split across the waves by head dims (the fixed pairwise tree of
+    // merge_split); every wave writes its dims of the records.  Lane (row i16, lg), tile dt, element i holds dim
+    // 16 (4 lg + i) + dt.
+    constexpr int TPW = 16 / WGW;
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
-        if (merge4(s_u.merge, wave, lane, m[rt], l[rt], o[rt])) {
-            const int r = 16 * (rt0 + rt) + i16;
-            const int qt = r / GRP, hh = r % GRP;
-            const float lt = half4_sum(l[rt]);
-            if (qpos[rt] >= 0) {
-                float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt) * GRP + hh) * REC;
-                if (lg == 0) {
-                    recp[0] = m[rt];
-                    recp[1] = lt;
-                }
-                // O^T C layout: lane (row i16, g) holds dims 16 (4 g + i) + dt
+        f4 om[TPW];
+        merge_split<WGW>(s_u.merge, wave, lane, m[rt], l[rt], o[rt], om);
+        const int r = 16 * (rt0 + rt) + i16;
+        const int qt = r / GRP, hh = r % GRP;
+        const float lt = half4_sum(l[rt]);
+        if (qpos[rt] >= 0) {
+            float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt) * GRP + hh) * REC;
+            if (wave == 0 && lg == 0) {
+                recp[0] = m[rt];
+                recp[1] = lt;
+            }
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float* dst = recp + 4 + 64 * lg + 16 * i;
+            for (int i = 0; i < 4; i++) {
+                float* dst = recp + 4 + 16 * (4 * lg + i) + TPW * wave;
+                if constexpr (TPW == 2) {
+                    *reinterpret_cast<float2*>(dst) = make_float2(om[0][i], om[1][i]);
+                } else {
 #pragma unroll
-                    for (int d4 = 0; d4 < 4; d4++)
-                        *reinterpret_cast<float4*>(dst + 4 * d4) = make_float4(
-                            o[rt][4 * d4][i], o[rt][4 * d4 + 1][i], o[rt][4 * d4 + 2][i], o[rt][4 * d4 + 3][i]);
+                    for (int t = 0; t < TPW; t++) dst[t] = om[t][i];
                 }
             }
         }
@@ -540,46 +554,6 @@ __device__ __forceinline__ h8 q4_codes(uint32_t w, const Q4Masks& k) {
     const uint32_t e26 = h2_bits(bits_h2((w8 & k.lo) | k.e_lo) - b_lo);
     const uint32_t e37 = h2_bits(bits_h2((w8 & k.hi) | k.e_hi) - b_hi);
     return make_h8(e04, e15, e26, e37);
-}
-
-// Merge of the partial states of the WGW waves of a workgroup, split across the waves by head dims: every wave puts
-// its state in LDS, then wave w folds the WGW states of the output tiles TPW w .. TPW w + TPW - 1 (TPW = 16 / WGW)
-// in the fixed tree fold(fold(c0, c1), fold(c2, c3)) (and fold(that, the same over c4..c7) for 8 waves).  Every
-// wave folds (m, l) along the same tree, so all of them hold the merged m and l.
-template <int WGW>
-struct MergeLdsN {
-    f4 o[WGW][16][64];
-    float ml[WGW][2][64];
-};
-
-template <int WGW>
-__device__ __forceinline__ void merge_split(MergeLdsN<WGW>& s, int wave, int lane, float& m, float& l, const f4* o,
-                                            f4* om) {
-    constexpr int TPW = 16 / WGW;
-    __syncthreads();  // every wave is done with the ring (or with the previous tile's merge)
-#pragma unroll
-    for (int dt = 0; dt < 16; dt++) s.o[wave][dt][lane] = o[dt];
-    s.ml[wave][0][lane] = m;
-    s.ml[wave][1][lane] = l;
-    __syncthreads();
-    float mm[WGW], ll[WGW];
-    f4 oo[WGW][TPW];
-#pragma unroll
-    for (int w = 0; w < WGW; w++) {
-        mm[w] = s.ml[w][0][lane];
-        ll[w] = s.ml[w][1][lane];
-#pragma unroll
-        for (int t = 0; t < TPW; t++) oo[w][t] = s.o[w][TPW * wave + t][lane];
-    }
-    // pairwise tree: level k folds state i with state i + 2^k into state i
-#pragma unroll
-    for (int step = 1; step < WGW; step *= 2)
-#pragma unroll
-        for (int w = 0; w < WGW; w += 2 * step) fold<TPW>(mm[w], ll[w], oo[w], mm[w + step], ll[w + step], oo[w + step]);
-    m = mm[0];
-    l = ll[0];
-#pragma unroll
-    for (int t = 0; t < TPW; t++) om[t] = oo[0][t];
 }
 
 // RT row tiles per wave, WGW waves per workgroup (WGW classes, one record).  RT = 1 keeps Q in registers; RT = 2
@@ -966,10 +940,11 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
     }
 }
 
-// Q4_0 decode workgroups: 8 waves, i.e. one workgroup per CU whose two waves on each SIMD belong to it (with two
-// 4-wave workgroups per CU the SIMD arbiter favours the older workgroup's waves for the whole kernel, and the younger
+// Decode workgroups: 8 waves, i.e. one workgroup per CU whose two waves on each SIMD belong to it (with two 4-wave
+// workgroups per CU the SIMD arbiter favours the older workgroup's waves for the whole kernel, and the younger
 // workgroup finishes alone at one wave per SIMD)
-constexpr int Q4_WGW = 8;
+constexpr int Q4_WGW = WG_CLASSES;
+constexpr int DEC_WGW = WG_CLASSES;
 
 template <int KVT>
 static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int nq, int nrec, float* work,
@@ -988,8 +963,13 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
                 hipLaunchKernelGGL((k_dec4<2, 1, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work,
                                    prof);
             }
+        } else if (t + 1 < rt) {
+            hipLaunchKernelGGL((k_dec<KVT, 2, DEC_WGW>), grid, dim3(64 * DEC_WGW), 0, st, q, kv, pos0, nq, t, work,
+                               prof);
+            t++;
         } else {
-            hipLaunchKernelGGL((k_dec<KVT, 1>), grid, dim3(256), 0, st, q, kv, pos0, nq, t, work, prof);
+            hipLaunchKernelGGL((k_dec<KVT, 1, DEC_WGW>), grid, dim3(64 * DEC_WGW), 0, st, q, kv, pos0, nq, t, work,
+                               prof);
         }
         profile_launched(prof, st);
     }
@@ -999,7 +979,7 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
                          void* work, float* out, const qwa_act_q8* oq, float* out_host, hipStream_t st) {
     // one record per workgroup; workgroups past the last chunk would hold no class with a chunk
     const int nchunk = (pos0 + nq - 1) / CHUNK + 1;
-    const int wgw = kvt == QWA_KV_Q4_0 ? Q4_WGW : WG_CLASSES;
+    const int wgw = kvt == QWA_KV_Q4_0 ? Q4_WGW : DEC_WGW;
     const int nsplit = min(DEC_CLASSES / wgw, (nchunk + wgw - 1) / wgw);
     float* w = static_cast<float*>(work);
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, w, st);
@@ -1022,7 +1002,7 @@ namespace qwa {
 #endif
 
 // ---- allocation-free decode: the partial records live in a file-scope device array instead of a work argument.
-// Its size is dec_work_bytes() (25.6 MB), which covers every valid call (up to 8 queries, any context up to
+// Its size is dec_work_bytes() (12.8 MB), which covers every valid call (up to 8 queries, any context up to
 // MAX_POS).  Every GPU holds its own copy at its own address, fetched once per device with hipGetSymbolAddress; host
 // code never passes the array's name itself to a kernel.  All calls on one GPU share the array: calls that overlap
 // on that GPU (different streams, or different threads without ordering) race on it.  The records need no clearing:
