@@ -214,6 +214,19 @@ def main():
                         max(5, args.steps // 5))
         extra["verify7_q4_32768_us_per_layer_graph"] = round(ms * 1000.0 / L, 3)
         del l3
+        # the other two cache formats at the headline context: decode and 7-query verify over 150000 positions
+        # (4 layers each, rotated; 1.3 GB (Q8_0) and 2.5 GB (F16) per rotation, past the MALL)
+        for kvo, nm in ((ops.Q8_0, "q8_0"), (ops.F16, "f16")):
+            lo = [fill_cache(ops, torch, kvo, n + 8, 4000 + 10 * kvo + i) for i in range(4)]
+            for nqo in (1, 7):
+                ms = time_graph(torch, lambda: [ops.attn_decode_multi(q, gate, kv, kvo, n + 7 - nqo, nqo, work, out)
+                                                for kv in lo], max(5, args.steps // 5))
+                us = ms * 1000.0 / len(lo)
+                extra[f"{'decode' if nqo == 1 else 'verify7'}_{nm}_150k_us_per_layer_graph"] = round(us, 3)
+                extra[f"{'decode' if nqo == 1 else 'verify7'}_{nm}_150k_gbs"] = round(
+                    (n + 7) * BYTES_PER_POS[kvo] / (us * 1e-6) / 1e9, 1)
+            del lo
+            torch.cuda.empty_cache()
         # C2: Q8_0 4096 decode with the new token's quantize-on-append (append + decode per layer)
         l2 = [fill_cache(ops, torch, ops.Q8_0, 4097, 3000 + i, 0.0) for i in range(L)]
         knew = torch.randn((1, 4, 256), device="cuda")
