@@ -96,7 +96,7 @@ int qwa_attn_decode_multi(const float* q, const float* gate, const qwa_kv_layer*
 
 /* No counterpart in the reference.  attn_decode_multi without the `work` argument, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the partial records
- * live in a static device array of the library (qwa_attn_work_bytes() bytes, 12.8 MB per GPU, held until the process
+ * live in a static device array of the library (qwa_attn_work_bytes() bytes, 25.6 MB per GPU, held until the process
  * ends), which covers every valid call.  The call allocates nothing.  All calls on one GPU share that array, so calls
  * that overlap on one GPU (different streams, unordered threads) race; results equal attn_decode_multi's bits. */
 int qwa_attn_decode_multi_noalloc(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int pos0, int nq,

@@ -49,12 +49,15 @@ constexpr int CGRP = 16;    // combine: records per fixed summation group
 constexpr int CHUNK = 16;   // keys per chunk
 constexpr int WG_CLASSES = 8;                   // classes (waves) per decode workgroup, every format
 constexpr int NREC = DEC_CLASSES / WG_CLASSES;  // records (workgroups) per KV head
+// record slots per KV head in the work buffer: a record, or (three-tile verify) its two halves, each the merge of 4
+// classes written by a 4-wave workgroup, that k_dec_combine folds into the record
+constexpr int NSLOT = 2 * NREC;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maximum (natural-log units)
 
 size_t dec_work_bytes(int n_pos) {
     (void)n_pos;
-    return (size_t)NREC * NKV * MAXQ * GRP * REC * sizeof(float);
+    return (size_t)NSLOT * NKV * MAXQ * GRP * REC * sizeof(float);
 }
 
 // One 16-key chunk in LDS.  K: piece-major, 16-byte piece p of row n at (16 p + n) * 16 (an MFMA operand read of one
@@ -188,6 +191,9 @@ template <int WGW>
 __device__ __forceinline__ void merge_split(MergeLdsN<WGW>& s, int wave, int lane, float& m, float& l, const f4* o,
                                             f4* om) {
     constexpr int TPW = 16 / WGW;
+    // a row's l is the sum of its 4 lanes' partial sums: reduced before any fold, so that the folds see the same
+    // values wherever they run (here, or in k_dec_combine for half records)
+    l = half4_sum(l);
     __syncthreads();  // every wave is done with the ring (or with the previous tile's merge)
 #pragma unroll
     for (int dt = 0; dt < 16; dt++) s.o[wave][dt][lane] = o[dt];
@@ -256,8 +262,11 @@ template <int KVT, int RT> struct DecCfg {
 // in every pass and every grouping), WGW waves (classes) per workgroup.  RT = 1 keeps Q in registers; RT = 2 reads
 // the Q fragments of both tiles from LDS at use (two tiles of Q and O would not fit two waves per SIMD), so each
 // chunk is streamed and unpacked once for both tiles.
-template <int KVT, int RT, int WGW>
-__global__ void __launch_bounds__(64 * WGW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// WPE waves per SIMD: 2, or 1 for the three-tile verify kernel (k_dec<KVT, 3, 4, 1>: O of three tiles takes 192
+// registers), whose 4-wave workgroups each write half a record (classes 8 r .. 8 r + 3 or 8 r + 4 .. 8 r + 7 of
+// record r, merged along the first two levels of the 8-class tree) into record slot 2 r or 2 r + 1.
+template <int KVT, int RT, int WGW, int WPE = 2>
+__global__ void __launch_bounds__(64 * WGW) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
       unsigned long long* prof) {
     prof_start(prof);
@@ -442,7 +451,7 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
         merge_split<WGW>(s_u.merge, wave, lane, m[rt], l[rt], o[rt], om);
         const int r = 16 * (rt0 + rt) + i16;
         const int qt = r / GRP, hh = r % GRP;
-        const float lt = half4_sum(l[rt]);
+        const float lt = l[rt];  // already summed over the row's lanes by merge_split
         if (qpos[rt] >= 0) {
             float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt) * GRP + hh) * REC;
             if (wave == 0 && lg == 0) {
@@ -829,7 +838,7 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
     for (int rt = 0; rt < RT; rt++) {
         f4 om[TPW];
         merge_split<WGW>(s_u.merge, wave, lane, m[rt], l[rt], o[rt], om);
-        const float lt = half4_sum(l[rt]);
+        const float lt = l[rt];  // already summed over the row's lanes by merge_split
         if (qpos[rt] >= 0) {
             float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt[rt]) * GRP + hh[rt]) * REC;
             if (wave == 0 && lg == 0) {
@@ -853,7 +862,9 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
 // Sums run over fixed groups of CGRP consecutive splits, in split order inside a group and in group order across
 // groups: the summation tree depends only on split indices, never on nq (splits past a query's window hold l = 0
 // and add exact zeros).
-__global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ work, int nsplit,
+// halves = 1: record s is the fold of slots 2 s and 2 s + 1 (the last level of the 8-class tree, the same
+// arithmetic as fold()), so a record has the same bits whichever kernel wrote it.
+__global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ work, int nsplit, int halves,
                                                      const float* __restrict__ gate, float* __restrict__ out,
                                                      float* __restrict__ out_host, qwa_act_q8 oq, int do_q) {
     constexpr int MAXSPLIT = NREC;
@@ -872,18 +883,42 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
     const int d = 64 * quarter + dim;
 
     // every load up front: this thread's O values (groups slice, slice + 4, ...) and one record's (m, l)
-    float ov[GPS][CGRP];
+    float ov[GPS][CGRP], ov2[GPS][CGRP];
+    const int ss = halves ? 2 : 1;  // slots per record
 #pragma unroll
     for (int k = 0; k < GPS; k++)
 #pragma unroll
         for (int i = 0; i < CGRP; i++) {
             const int s = (slice + 4 * k) * CGRP + i;
-            ov[k][i] = s < nsplit ? base[s * sstride + 4 + d] : 0.0f;
+            ov[k][i] = s < nsplit ? base[(size_t)ss * s * sstride + 4 + d] : 0.0f;
+            ov2[k][i] = s < nsplit && halves ? base[(size_t)(2 * s + 1) * sstride + 4 + d] : 0.0f;
         }
     float ms = -INFINITY, ls = 0.0f;
     if (tid < nsplit) {
-        ms = base[tid * sstride];
-        ls = base[tid * sstride + 1];
+        ms = base[(size_t)ss * tid * sstride];
+        ls = base[(size_t)ss * tid * sstride + 1];
+    }
+    if (halves) {
+        __shared__ float s_fa[MAXSPLIT], s_fb[MAXSPLIT];
+        if (tid < nsplit) {
+            // fold(): M = max(m, m2), factors exp2((m - M') log2 e) with M' = 0 when M = -inf
+            const float m2 = base[(size_t)(2 * tid + 1) * sstride], l2 = base[(size_t)(2 * tid + 1) * sstride + 1];
+            const float M = fmaxf(ms, m2);
+            const float Ms = M == -INFINITY ? 0.0f : M;
+            const float fa = fast_exp2((ms - Ms) * LOG2E), fb = fast_exp2((m2 - Ms) * LOG2E);
+            ls = fmaf(ls, fa, l2 * fb);
+            ms = M;
+            s_fa[tid] = fa;
+            s_fb[tid] = fb;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < GPS; k++)
+#pragma unroll
+            for (int i = 0; i < CGRP; i++) {
+                const int s = (slice + 4 * k) * CGRP + i;
+                if (s < nsplit) ov[k][i] = fmaf(ov[k][i], s_fa[s], ov2[k][i] * s_fb[s]);
+            }
     }
     // global max over records that saw keys, then each record's factor exp(m - M) (0 for empty records)
     float mx = wave_max(ls > 0.0f ? ms : -INFINITY);
@@ -945,6 +980,28 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
 // workgroup finishes alone at one wave per SIMD)
 constexpr int Q4_WGW = WG_CLASSES;
 constexpr int DEC_WGW = WG_CLASSES;
+#ifndef QWA_DEC3
+#define QWA_DEC3 1
+#endif
+// F16: three row tiles (6..8 queries) in one pass at one wave per SIMD.  (Q8_0 measured slower that way, 247 against
+// 155 us per 7-query layer at 150000 positions: its conversion work no longer hides behind a second wave, and the
+// kernel spills; it keeps two passes.)
+constexpr bool PF3_VERIFY = QWA_DEC3 != 0;
+
+// The one-pass three-tile verify kernel where it is used (F16, 6..8 queries); false if the call takes the passes of
+// one or two tiles.  The kernel's 4-wave workgroups write half records into 2 nrec slots per KV head.
+template <int KVT>
+static bool dec3_pass(int rt, const float* q, const qwa_kv_layer& kv, int pos0, int nq, int t, int nrec, float* work,
+                      unsigned long long* prof, hipStream_t st) {
+    if constexpr (KVT == QWA_KV_F16) {
+        if (PF3_VERIFY && rt == 3) {
+            hipLaunchKernelGGL((k_dec<KVT, 3, 4, 1>), dim3(2 * nrec, NKV), dim3(256), 0, st, q, kv, pos0, nq, t, work,
+                               prof);
+            return true;
+        }
+    }
+    return false;
+}
 
 template <int KVT>
 static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int nq, int nrec, float* work,
@@ -952,7 +1009,8 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
     const int rt = (GRP * nq + 15) / 16;
     const dim3 grid(nrec, NKV);
     for (int t = 0; t < rt; t++) {
-        unsigned long long* prof = profile_slot(nrec * NKV, st);
+        const bool three = KVT == QWA_KV_F16 && PF3_VERIFY && rt == 3;  // one pass of 2 nrec half-record workgroups
+        unsigned long long* prof = profile_slot((three ? 2 : 1) * nrec * NKV, st);
         if constexpr (KVT == QWA_KV_Q4_0) {
             // two row tiles share one pass over the cache; a third tile gets a pass of its own
             if (t + 1 < rt) {
@@ -963,6 +1021,8 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
                 hipLaunchKernelGGL((k_dec4<2, 1, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work,
                                    prof);
             }
+        } else if (dec3_pass<KVT>(rt, q, kv, pos0, nq, t, nrec, work, prof, st)) {
+            t += 2;
         } else if (t + 1 < rt) {
             hipLaunchKernelGGL((k_dec<KVT, 2, DEC_WGW>), grid, dim3(64 * DEC_WGW), 0, st, q, kv, pos0, nq, t, work,
                                prof);
@@ -988,7 +1048,8 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const qwa_act_q8 a = oq ? *oq : qwa_act_q8{nullptr, nullptr, nullptr};
-    hipLaunchKernelGGL(k_dec_combine, dim3(nq * NH, 4), dim3(256), 0, st, w, nsplit, gate, out, out_host, a,
+    const int halves = PF3_VERIFY && kvt == QWA_KV_F16 && (GRP * nq + 15) / 16 == 3;
+    hipLaunchKernelGGL(k_dec_combine, dim3(nq * NH, 4), dim3(256), 0, st, w, nsplit, halves, gate, out, out_host, a,
                        oq != nullptr ? 1 : 0);
     return hipGetLastError();
 }
@@ -1002,12 +1063,12 @@ namespace qwa {
 #endif
 
 // ---- allocation-free decode: the partial records live in a file-scope device array instead of a work argument.
-// Its size is dec_work_bytes() (12.8 MB), which covers every valid call (up to 8 queries, any context up to
+// Its size is dec_work_bytes() (25.6 MB), which covers every valid call (up to 8 queries, any context up to
 // MAX_POS).  Every GPU holds its own copy at its own address, fetched once per device with hipGetSymbolAddress; host
 // code never passes the array's name itself to a kernel.  All calls on one GPU share the array: calls that overlap
 // on that GPU (different streams, or different threads without ordering) race on it.  The records need no clearing:
 // every record a combine reads is written by the same call first.
-constexpr size_t DEC_SCRATCH_FLOATS = (size_t)NREC * NKV * MAXQ * GRP * REC;
+constexpr size_t DEC_SCRATCH_FLOATS = (size_t)NSLOT * NKV * MAXQ * GRP * REC;
 static __device__ __align__(256) float scratch[DEC_SCRATCH_FLOATS];
 
 size_t dec_scratch_bytes() { return DEC_SCRATCH_FLOATS * sizeof(float); }
