@@ -225,6 +225,25 @@ def test_decode_in_hip_graph(gpu):
     del g
 
 
+@pytest.mark.parametrize("kvt,nq", [(ops.F16, 7), (ops.F16, 4), (ops.Q8_0, 7), (ops.Q8_0, 5)],
+                         ids=["f16-nq7", "f16-nq4", "q8_0-nq7", "q8_0-nq5"])
+def test_verify_passes_long_context(gpu, oracle, kvt, nq):
+    """The verify kernels at a context with several chunks per class: F16 with 6..8 queries in its one-pass
+    three-tile kernel (half records folded by the combine), 4..5 queries in the two-tile pass, Q8_0 7 queries as two
+    passes; against the oracle, and each query bit-identical to its one-query decode."""
+    pos0 = 40000
+    print(f"verify long context kvt={KV_NAMES[kvt]} nq={nq}", flush=True)
+    kv, _, _ = make_cache(kvt, pos0 + nq, pos0 + nq, seed=90 + nq)
+    q, gate = _qg(nq, 91 + nq)
+    out = _decode(kv, q, gate, pos0, nq).cpu().numpy()
+    Kd, Vd = dequant_cache(kv, pos0 + nq)
+    ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, pos0, nq)
+    assert_close(out, ref, f"verify {KV_NAMES[kvt]} nq={nq} at {pos0}")
+    for t in (0, nq - 1):
+        one = _decode(kv, q[t:t + 1].contiguous(), gate[t:t + 1].contiguous(), pos0 + t, 1).cpu().numpy()
+        assert np.array_equal(out[t].view(np.uint32), one[0].view(np.uint32)), t
+
+
 @pytest.mark.parametrize("kvt,nq", [(ops.Q4_0, 8), (ops.F16, 1), (ops.Q8_0, 3)],
                          ids=["q4_0-nq8", "f16-nq1", "q8_0-nq3"])
 def test_decode_at_max_positions(gpu, oracle, kvt, nq):
