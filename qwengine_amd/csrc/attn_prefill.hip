@@ -26,6 +26,9 @@
 
 namespace qwa {
 
+#ifndef QWA_PF_XCD
+#define QWA_PF_XCD 1
+#endif
 #ifndef QWA_PF_WAVES
 #define QWA_PF_WAVES 8
 #endif
@@ -331,7 +334,16 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
     __shared__ __attribute__((aligned(16))) _Float16 s_vt[IMG ? 1 : 2][IMG ? 8 : HD * VT_LD];
     const int t = threadIdx.x, lane = t & 63, i16 = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane((int)(t >> 6));
+#if QWA_PF_XCD
+    // XCD-aware numbering: workgroup lin is dispatched to XCD lin % 8; give each XCD 4 whole (KV head, split) pairs, so
+    // the row blocks that read the same image tiles share one L2
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int xcd = lin & 7, slot = lin >> 3, nrb = gridDim.x;
+    const int pair = 4 * xcd + slot / nrb;
+    const int bx = slot % nrb, g = pair % NKV, sp = pair / NKV;
+#else
     const int bx = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
+#endif
     const int row0 = bx * PF_ROWS;
     const int nrows = GRP * B;
     // last key any row of the workgroup sees, and this split's tiles [tb, tb + nt) of the row block's range
