@@ -987,14 +987,17 @@ constexpr int DEC_WGW = WG_CLASSES;
 // 155 us per 7-query layer at 150000 positions: its conversion work no longer hides behind a second wave, and the
 // kernel spills; it keeps two passes.)
 constexpr bool PF3_VERIFY = QWA_DEC3 != 0;
+// below this context the two-pass path is faster (measured, 7 queries: 30.9 vs 35.1 us at 4096 positions, 67.5 vs
+// 70.5 at 32768; the one-pass kernel wins from ~48K: 104.5 vs 110.6 at 65536, 190 vs 236 at 150000)
+constexpr int DEC3_MIN_POS = 49152;
 
 // The one-pass three-tile verify kernel where it is used (F16, 6..8 queries); false if the call takes the passes of
 // one or two tiles.  The kernel's 4-wave workgroups write half records into 2 nrec slots per KV head.
 template <int KVT>
-static bool dec3_pass(int rt, const float* q, const qwa_kv_layer& kv, int pos0, int nq, int t, int nrec, float* work,
-                      unsigned long long* prof, hipStream_t st) {
+static bool dec3_pass(bool three, const float* q, const qwa_kv_layer& kv, int pos0, int nq, int t, int nrec,
+                      float* work, unsigned long long* prof, hipStream_t st) {
     if constexpr (KVT == QWA_KV_F16) {
-        if (PF3_VERIFY && rt == 3) {
+        if (three) {
             hipLaunchKernelGGL((k_dec<KVT, 3, 4, 1>), dim3(2 * nrec, NKV), dim3(256), 0, st, q, kv, pos0, nq, t, work,
                                prof);
             return true;
@@ -1004,13 +1007,12 @@ static bool dec3_pass(int rt, const float* q, const qwa_kv_layer& kv, int pos0, 
 }
 
 template <int KVT>
-static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int nq, int nrec, float* work,
-                           hipStream_t st) {
+static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int nq, int nrec, bool three,
+                           float* work, hipStream_t st) {
     const int rt = (GRP * nq + 15) / 16;
     const dim3 grid(nrec, NKV);
     for (int t = 0; t < rt; t++) {
-        const bool three = KVT == QWA_KV_F16 && PF3_VERIFY && rt == 3;  // one pass of 2 nrec half-record workgroups
-        unsigned long long* prof = profile_slot((three ? 2 : 1) * nrec * NKV, st);
+        unsigned long long* prof = profile_slot((three ? 2 : 1) * nrec * NKV, st);  // three: 2 nrec half records
         if constexpr (KVT == QWA_KV_Q4_0) {
             // two row tiles share one pass over the cache; a third tile gets a pass of its own
             if (t + 1 < rt) {
@@ -1021,7 +1023,7 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
                 hipLaunchKernelGGL((k_dec4<2, 1, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work,
                                    prof);
             }
-        } else if (dec3_pass<KVT>(rt, q, kv, pos0, nq, t, nrec, work, prof, st)) {
+        } else if (dec3_pass<KVT>(three, q, kv, pos0, nq, t, nrec, work, prof, st)) {
             t += 2;
         } else if (t + 1 < rt) {
             hipLaunchKernelGGL((k_dec<KVT, 2, DEC_WGW>), grid, dim3(64 * DEC_WGW), 0, st, q, kv, pos0, nq, t, work,
@@ -1042,14 +1044,16 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     const int wgw = kvt == QWA_KV_Q4_0 ? Q4_WGW : DEC_WGW;
     const int nsplit = min(DEC_CLASSES / wgw, (nchunk + wgw - 1) / wgw);
     float* w = static_cast<float*>(work);
-    if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, w, st);
-    else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, w, st);
-    else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, w, st);
+    // F16 with 6..8 queries from DEC3_MIN_POS positions on: the one-pass three-tile kernel (every path gives the
+    // same bits, so the choice may depend on the context)
+    const bool three = PF3_VERIFY && kvt == QWA_KV_F16 && (GRP * nq + 15) / 16 == 3 && pos0 + nq >= DEC3_MIN_POS;
+    if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, three, w, st);
+    else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, false, w, st);
+    else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, false, w, st);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const qwa_act_q8 a = oq ? *oq : qwa_act_q8{nullptr, nullptr, nullptr};
-    const int halves = PF3_VERIFY && kvt == QWA_KV_F16 && (GRP * nq + 15) / 16 == 3;
-    hipLaunchKernelGGL(k_dec_combine, dim3(nq * NH, 4), dim3(256), 0, st, w, nsplit, halves, gate, out, out_host, a,
+    hipLaunchKernelGGL(k_dec_combine, dim3(nq * NH, 4), dim3(256), 0, st, w, nsplit, three ? 1 : 0, gate, out, out_host, a,
                        oq != nullptr ? 1 : 0);
     return hipGetLastError();
 }
