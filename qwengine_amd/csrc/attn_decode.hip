@@ -181,6 +181,18 @@ __device__ __forceinline__ float half4_sum(float x) {
 // its state in LDS, then wave w folds the WGW states of the output tiles TPW w .. TPW w + TPW - 1 (TPW = 16 / WGW)
 // in the fixed tree fold(fold(c0, c1), fold(c2, c3)) (and fold(that, the same over c4..c7) for 8 waves).  Every
 // wave folds (m, l) along the same tree, so all of them hold the merged m and l.
+// The two waves of a SIMD (w and w + WGW / 2 of a workgroup) stream classes of equal length, but the SIMD's
+// arbiter favours the older one, and the younger one then finishes its last chunks alone.  Each wave publishes its
+// chunk index; the one that is behind takes issue priority until it has caught up.  (Priority only orders issue
+// between the two waves; the arithmetic is unchanged.)
+template <int WGW>
+__device__ __forceinline__ void pair_priority(int* s_prog, int wave, int lane, int j) {
+    if (lane == 0) s_prog[wave] = j;
+    const int other = s_prog[wave ^ (WGW / 2)];
+    if (j < other) __builtin_amdgcn_s_setprio(2);
+    else __builtin_amdgcn_s_setprio(0);
+}
+
 template <int WGW>
 struct MergeLdsN {
     f4 o[WGW][16][64];
@@ -273,11 +285,14 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     using C = ChunkLds<KVT>;
     constexpr int NST = DecCfg<KVT, RT>::NST;
     constexpr bool QLDS = RT > 1;
+    // pair_priority wherever two waves share a SIMD and its 32 bytes fit (not the F16 two-tile kernel, at 160 KB)
+    constexpr bool PRIO = WPE == 2 && RT * 8 * 2 * 64 * 16 + WGW * NST * C::BYTES + 4 * WGW <= 163840;
     // the Q fragments and the chunk ring of every wave while streaming; the partial states while merging
     __shared__ __attribute__((aligned(16))) union {
         struct {
             h8 q[RT * 8 * 2 * 64];  // [rt][block][hi, lo][lane]
             uint8_t ring[WGW][NST][C::BYTES];
+            int prog[PRIO ? WGW : 0];  // chunk index of each wave (pair_priority)
         } a;
         MergeLdsN<WGW> merge;
     } s_u;
@@ -334,6 +349,7 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
 
     if (nmine > 0) {
         for (int j = 0; j < nmine; j++) {
+            if constexpr (PRIO) pair_priority<WGW>(s_u.a.prog, wave, lane, j);
             const int slot = j % NST;
             const int kb = chunk_key(j);
             wait_vmcnt<C::NLOAD * (NST - 1)>();  // this slot has landed; the later ones may still fly
@@ -439,6 +455,7 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
         }
         wait_vmcnt<0>();  // drain the clamped prefetches before the ring is reused or the wave exits
     }
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     TRACE(3);
 
     // ---- merge the WGW classes of each row tile, split across the waves by head dims (the fixed pairwise tree of
@@ -582,6 +599,7 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
         } a;
         MergeLdsN<WGW> merge;
     } s_u;
+    __shared__ int s_prog[WGW];  // chunk index of each wave (pair_priority)
     h8* s_q = s_u.a.q;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -781,6 +799,7 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
                 if (NST < nmine) issue(NST);
             }
             for (int j = 0; j + 1 < nmine; j++) {
+                pair_priority<WGW>(s_prog, wave, lane, j);
 #ifdef QWA_TRACE
                 tw = __builtin_amdgcn_s_memtime();
 #endif
@@ -810,6 +829,7 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
 #endif
         } else {
             for (int j = 0; j < nmine; j++) {
+                pair_priority<WGW>(s_prog, wave, lane, j);
                 if (j + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
                 else wait_vmcnt<0>();
                 // two row tiles: V is read after the softmax, so K and V registers are never live together
@@ -831,6 +851,7 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
         }
     }
 
+    __builtin_amdgcn_s_setprio(0);
     // ---- merge the WGW classes of each row tile, split across the waves by head dims; every wave writes its dims of
     // the records.  Lane (row i16, lg), tile 2 b + par, element i holds dim 32 b + 8 lg + 2 i + par.
     constexpr int TPW = 16 / WGW;
