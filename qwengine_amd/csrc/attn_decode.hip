@@ -379,11 +379,13 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
                 for (int rt = 0; rt < RT; rt++) {
                     const h8 bh = QLDS ? s_q[((rt * 8 + b) * 2 + 0) * 64 + lane] : qh[QLDS ? 0 : rt][b];
                     const h8 bl = QLDS ? s_q[((rt * 8 + b) * 2 + 1) * 64 + lane] : ql[QLDS ? 0 : rt][b];
-                    f4 a = mfma16(ka, bh, f4{0.0f, 0.0f, 0.0f, 0.0f});
-                    a = mfma16(ka, bl, a);
                     if constexpr (KVT == QWA_KV_F16) {
-                        S[rt] += a;
+                        // no block scale: the blocks accumulate in the MFMA accumulator (no VALU adds, and the
+                        // three-tile kernel no longer spills)
+                        S[rt] = mfma16(ka, bl, mfma16(ka, bh, S[rt]));
                     } else {
+                        f4 a = mfma16(ka, bh, f4{0.0f, 0.0f, 0.0f, 0.0f});
+                        a = mfma16(ka, bl, a);
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
                             const float d = h2f_bits((uint16_t)(kd[i][b >> 1] >> (16 * (b & 1))));
@@ -1004,13 +1006,11 @@ constexpr int DEC_WGW = WG_CLASSES;
 #ifndef QWA_DEC3
 #define QWA_DEC3 1
 #endif
-// F16: three row tiles (6..8 queries) in one pass at one wave per SIMD.  (Q8_0 measured slower that way, 247 against
-// 155 us per 7-query layer at 150000 positions: its conversion work no longer hides behind a second wave, and the
-// kernel spills; it keeps two passes.)
+// F16: three row tiles (6..8 queries) in one pass at one wave per SIMD, at every context (7 queries: 25.4 against
+// 30.3 us per layer at 4096 positions, 48.7 / 47.8 at 16384, 63.5 / 67.9 at 32768, 88.5 / 109.7 at 65536 for one pass
+// / two passes).  (Q8_0 measured slower that way, 247 against 155 us per 7-query layer at 150000 positions: its
+// conversion work no longer hides behind a second wave, and the kernel spills; it keeps two passes.)
 constexpr bool PF3_VERIFY = QWA_DEC3 != 0;
-// below this context the two-pass path is faster (measured, 7 queries: 30.9 vs 35.1 us at 4096 positions, 67.5 vs
-// 70.5 at 32768; the one-pass kernel wins from ~48K: 104.5 vs 110.6 at 65536, 190 vs 236 at 150000)
-constexpr int DEC3_MIN_POS = 49152;
 
 // The one-pass three-tile verify kernel where it is used (F16, 6..8 queries); false if the call takes the passes of
 // one or two tiles.  The kernel's 4-wave workgroups write half records into 2 nrec slots per KV head.
@@ -1065,9 +1065,8 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     const int wgw = kvt == QWA_KV_Q4_0 ? Q4_WGW : DEC_WGW;
     const int nsplit = min(DEC_CLASSES / wgw, (nchunk + wgw - 1) / wgw);
     float* w = static_cast<float*>(work);
-    // F16 with 6..8 queries from DEC3_MIN_POS positions on: the one-pass three-tile kernel (every path gives the
-    // same bits, so the choice may depend on the context)
-    const bool three = PF3_VERIFY && kvt == QWA_KV_F16 && (GRP * nq + 15) / 16 == 3 && pos0 + nq >= DEC3_MIN_POS;
+    // F16 with 6..8 queries: the one-pass three-tile kernel (every path gives the same bits)
+    const bool three = PF3_VERIFY && kvt == QWA_KV_F16 && (GRP * nq + 15) / 16 == 3;
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, three, w, st);
     else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, false, w, st);
     else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, false, w, st);

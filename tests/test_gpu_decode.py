@@ -229,9 +229,8 @@ def test_decode_in_hip_graph(gpu):
                          ids=["f16-nq7", "f16-nq4", "q8_0-nq7", "q8_0-nq5"])
 def test_verify_passes_long_context(gpu, oracle, kvt, nq):
     """The verify kernels at a context with several chunks per class: F16 with 6..8 queries in its one-pass
-    three-tile kernel (used from 49152 positions on; half records folded by the combine), 4..5 queries in the
-    two-tile pass, Q8_0 7 queries as two passes; against the oracle, and each query bit-identical to its one-query
-    decode."""
+    three-tile kernel (half records folded by the combine), 4..5 queries in the two-tile pass, Q8_0 7 queries as two
+    passes; against the oracle, and each query bit-identical to its one-query decode."""
     pos0 = 50000
     print(f"verify long context kvt={KV_NAMES[kvt]} nq={nq}", flush=True)
     kv, _, _ = make_cache(kvt, pos0 + nq, pos0 + nq, seed=90 + nq)
@@ -240,7 +239,7 @@ def test_verify_passes_long_context(gpu, oracle, kvt, nq):
     Kd, Vd = dequant_cache(kv, pos0 + nq)
     ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, pos0, nq)
     assert_close(out, ref, f"verify {KV_NAMES[kvt]} nq={nq} at {pos0}")
-    # the same queries below the three-tile threshold (two passes) give the same bits as well
+    # a second context, with a partly filled last round of chunks
     if kvt == ops.F16 and nq >= 6:
         kv2, _, _ = make_cache(kvt, 30000 + nq, 30000 + nq, seed=93)
         q2, g2 = _qg(nq, 94)
