@@ -43,9 +43,15 @@ def _hipcc() -> str:
     return "hipcc"
 
 
+# per-source flags.  attn_decode.hip: MFMA results in VGPRs wherever the register budget allows.  Its one-wave-per-SIMD
+# verify kernels otherwise get their score MFMAs written to accumulation registers, and every block's product is then
+# copied out for its scale multiply (the Q8_0 three-tile kernel spilled 77 registers that way).
+FILE_FLAGS = {"attn_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str, extra: list[str], obj_dir: str) -> str:
     obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr[-6000:]}")

@@ -1006,18 +1006,19 @@ constexpr int DEC_WGW = WG_CLASSES;
 #ifndef QWA_DEC3
 #define QWA_DEC3 1
 #endif
-// F16: three row tiles (6..8 queries) in one pass at one wave per SIMD, at every context (7 queries: 25.4 against
-// 30.3 us per layer at 4096 positions, 48.7 / 47.8 at 16384, 63.5 / 67.9 at 32768, 88.5 / 109.7 at 65536 for one pass
-// / two passes).  (Q8_0 measured slower that way, 247 against 155 us per 7-query layer at 150000 positions: its
-// conversion work no longer hides behind a second wave, and the kernel spills; it keeps two passes.)
+// Three row tiles (6..8 queries) in one pass at one wave per SIMD.  F16 at every context (7 queries, one pass / two
+// passes: 25.4 / 30.3 us per layer at 4096 positions, 48.7 / 47.8 at 16384, 63.5 / 67.9 at 32768, 88.5 / 109.7 at
+// 65536).  Q8_0, whose int8 conversion hides behind a second wave in the two-tile pass, only below 8192 and from
+// 98304 positions on (19.4 / 27.0 at 4096, 41.2 / 36.6 at 16384, 53.8 / 51.4 at 32768, 65.6 / 61.7 at 49152,
+// 77.0 / 77.1 at 65536, 139 / 149 at 150000).  Q4_0 keeps two passes.
 constexpr bool PF3_VERIFY = QWA_DEC3 != 0;
 
-// The one-pass three-tile verify kernel where it is used (F16, 6..8 queries); false if the call takes the passes of
-// one or two tiles.  The kernel's 4-wave workgroups write half records into 2 nrec slots per KV head.
+// The one-pass three-tile verify kernel where it is used (F16 or Q8_0, 6..8 queries); false if the call takes the
+// passes of one or two tiles.  The kernel's 4-wave workgroups write half records into 2 nrec slots per KV head.
 template <int KVT>
 static bool dec3_pass(bool three, const float* q, const qwa_kv_layer& kv, int pos0, int nq, int t, int nrec,
                       float* work, unsigned long long* prof, hipStream_t st) {
-    if constexpr (KVT == QWA_KV_F16) {
+    if constexpr (KVT != QWA_KV_Q4_0) {
         if (three) {
             hipLaunchKernelGGL((k_dec<KVT, 3, 4, 1>), dim3(2 * nrec, NKV), dim3(256), 0, st, q, kv, pos0, nq, t, work,
                                prof);
@@ -1065,10 +1066,12 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     const int wgw = kvt == QWA_KV_Q4_0 ? Q4_WGW : DEC_WGW;
     const int nsplit = min(DEC_CLASSES / wgw, (nchunk + wgw - 1) / wgw);
     float* w = static_cast<float*>(work);
-    // F16 with 6..8 queries: the one-pass three-tile kernel (every path gives the same bits)
-    const bool three = PF3_VERIFY && kvt == QWA_KV_F16 && (GRP * nq + 15) / 16 == 3;
+    // 6..8 queries: the one-pass three-tile kernel where it is the faster path (every path gives the same bits)
+    const int npos = pos0 + nq;
+    const bool three = PF3_VERIFY && (GRP * nq + 15) / 16 == 3 &&
+                       (kvt == QWA_KV_F16 || (kvt == QWA_KV_Q8_0 && (npos < 8192 || npos >= 98304)));
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, three, w, st);
-    else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, false, w, st);
+    else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, three, w, st);
     else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, false, w, st);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
