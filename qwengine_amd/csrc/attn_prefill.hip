@@ -335,11 +335,12 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
     const int t = threadIdx.x, lane = t & 63, i16 = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane((int)(t >> 6));
 #if QWA_PF_XCD
-    // XCD-aware numbering: workgroup lin is dispatched to XCD lin % 8; give each XCD 4 whole (KV head, split) pairs, so
+    // XCD-aware numbering: workgroup lin is dispatched to XCD lin % 8; give each XCD whole (KV head, split) pairs, so
     // the row blocks that read the same image tiles share one L2
     const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
     const int xcd = lin & 7, slot = lin >> 3, nrb = gridDim.x;
-    const int pair = 4 * xcd + slot / nrb;
+    static_assert(NKV * PF_NS % 8 == 0, "whole (KV head, split) pairs per XCD");
+    const int pair = NKV * PF_NS / 8 * xcd + slot / nrb;
     const int bx = slot % nrb, g = pair % NKV, sp = pair / NKV;
 #else
     const int bx = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
