@@ -589,24 +589,30 @@ __device__ __forceinline__ h8 q4_codes(uint32_t w, const Q4Masks& k) {
 // are unpacked once for both tiles while the wave still fits two per SIMD.  A row's arithmetic is the same whatever
 // RT is.
 template <int NST, int RT, int WGW>
-__global__ void __launch_bounds__(WGW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
-       unsigned long long* prof) {
-    prof_start(prof);
-    constexpr bool QLDS = RT > 1;
-    __shared__ __attribute__((aligned(16))) union {
+struct Dec4Lds {
+    union {
         struct {
             h8 q[RT * 8 * 2 * 64];  // [rt][block][hi, lo][lane]
             uint8_t ring[WGW][NST][Q4Chunk::BYTES];
         } a;
         MergeLdsN<WGW> merge;
-    } s_u;
-    __shared__ int s_prog[WGW];  // chunk index of each wave (pair_priority)
+    } u;
+    int prog[WGW];  // chunk index of each wave (pair_priority)
+};
+
+// One workgroup (record rec of KV head g) of the Q4_0 decode; its LDS is s.
+template <int NST, int RT, int WGW>
+__device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float* __restrict__ q, const qwa_kv_layer& kv,
+                                          int pos0, int nq, int rt0, float* __restrict__ work, int rec, int g,
+                                          unsigned long long* prof) {
+    prof_start(prof);
+    constexpr bool QLDS = RT > 1;
+    auto& s_u = s.u;
+    int* s_prog = s.prog;
     h8* s_q = s_u.a.q;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
-    const int g = blockIdx.y, rec = blockIdx.x;
     const int kmax = pos0 + nq - 1;
     const int nchunk = kmax / CHUNK + 1;
     const int cls = rec * WGW + wave;
@@ -881,6 +887,30 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
     prof_end(prof);
 }
 
+template <int NST, int RT, int WGW>
+__global__ void __launch_bounds__(WGW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
+       unsigned long long* prof) {
+    __shared__ __attribute__((aligned(16))) Dec4Lds<NST, RT, WGW> s;
+    dec4_body<NST, RT, WGW>(s, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, prof);
+}
+
+// The two passes of a three-tile verify in one launch, grid (records, NKV, 2): z = 0 takes row tiles rt0 and rt0 + 1,
+// z = 1 tile rt0 + 2.  The two-tile workgroups are dispatched first; the one-tile ones fill the CUs as they free up,
+// with no drain and ramp between two launches.  Each workgroup runs exactly the code of its own pass.
+template <int WGW>
+__global__ void __launch_bounds__(WGW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_dec4_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
+         unsigned long long* prof) {
+    __shared__ __attribute__((aligned(16))) union {
+        Dec4Lds<2, 2, WGW> two;
+        Dec4Lds<2, 1, WGW> one;
+    } s;
+    if (blockIdx.z == 0) dec4_body<2, 2, WGW>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, prof);
+    else dec4_body<2, 1, WGW>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, prof);
+}
+
+
 // Combine: one workgroup per (query t, head h, quarter of the head dims).  256 threads = 64 dims x 4 slices.
 // Sums run over fixed groups of CGRP consecutive splits, in split order inside a group and in group order across
 // groups: the summation tree depends only on split indices, never on nq (splits past a query's window hold l = 0
@@ -1003,6 +1033,11 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
 // workgroup finishes alone at one wave per SIMD)
 constexpr int Q4_WGW = WG_CLASSES;
 constexpr int DEC_WGW = WG_CLASSES;
+#ifndef QWA_Q4_ONE_LAUNCH
+#define QWA_Q4_ONE_LAUNCH 1
+#endif
+// 6..8-query Q4_0 verify: both passes (two tiles, one tile) as one launch
+constexpr bool Q4_ONE_LAUNCH = QWA_Q4_ONE_LAUNCH != 0;
 #ifndef QWA_DEC3
 #define QWA_DEC3 1
 #endif
@@ -1034,9 +1069,18 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
     const int rt = (GRP * nq + 15) / 16;
     const dim3 grid(nrec, NKV);
     for (int t = 0; t < rt; t++) {
+        if constexpr (KVT == QWA_KV_Q4_0) {
+            // two row tiles share one pass over the cache; a third tile gets a pass of its own, in the same launch
+            if (Q4_ONE_LAUNCH && t == 0 && rt == 3) {
+                unsigned long long* prof = profile_slot(2 * nrec * NKV, st);
+                hipLaunchKernelGGL((k_dec4_3<Q4_WGW>), dim3(nrec, NKV, 2), dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq,
+                                   0, work, prof);
+                profile_launched(prof, st);
+                break;
+            }
+        }
         unsigned long long* prof = profile_slot((three ? 2 : 1) * nrec * NKV, st);  // three: 2 nrec half records
         if constexpr (KVT == QWA_KV_Q4_0) {
-            // two row tiles share one pass over the cache; a third tile gets a pass of its own
             if (t + 1 < rt) {
                 hipLaunchKernelGGL((k_dec4<2, 2, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work,
                                    prof);
