@@ -277,28 +277,36 @@ template <int KVT, int RT> struct DecCfg {
 // WPE waves per SIMD: 2, or 1 for the three-tile verify kernel (k_dec<KVT, 3, 4, 1>: O of three tiles takes 192
 // registers), whose 4-wave workgroups each write half a record (classes 8 r .. 8 r + 3 or 8 r + 4 .. 8 r + 7 of
 // record r, merged along the first two levels of the 8-class tree) into record slot 2 r or 2 r + 1.
-template <int KVT, int RT, int WGW, int WPE = 2>
-__global__ void __launch_bounds__(64 * WGW) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
-      unsigned long long* prof) {
-    prof_start(prof);
+template <int KVT, int RT, int WGW, int WPE>
+struct DecLds {
     using C = ChunkLds<KVT>;
-    constexpr int NST = DecCfg<KVT, RT>::NST;
-    constexpr bool QLDS = RT > 1;
+    static constexpr int NST = DecCfg<KVT, RT>::NST;
     // pair_priority wherever two waves share a SIMD and its 32 bytes fit (not the F16 two-tile kernel, at 160 KB)
-    constexpr bool PRIO = WPE == 2 && RT * 8 * 2 * 64 * 16 + WGW * NST * C::BYTES + 4 * WGW <= 163840;
+    static constexpr bool PRIO = WPE == 2 && RT * 8 * 2 * 64 * 16 + WGW * NST * C::BYTES + 4 * WGW <= 163840;
     // the Q fragments and the chunk ring of every wave while streaming; the partial states while merging
-    __shared__ __attribute__((aligned(16))) union {
+    union {
         struct {
             h8 q[RT * 8 * 2 * 64];  // [rt][block][hi, lo][lane]
             uint8_t ring[WGW][NST][C::BYTES];
             int prog[PRIO ? WGW : 0];  // chunk index of each wave (pair_priority)
         } a;
         MergeLdsN<WGW> merge;
-    } s_u;
+    } u;
+};
+
+// One workgroup (record rec of KV head g) of the F16 / Q8_0 decode; its LDS is s.
+template <int KVT, int RT, int WGW, int WPE>
+__device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const float* __restrict__ q,
+                                         const qwa_kv_layer& kv, int pos0, int nq, int rt0, float* __restrict__ work,
+                                         int rec, int g, unsigned long long* prof) {
+    prof_start(prof);
+    using C = ChunkLds<KVT>;
+    constexpr int NST = DecCfg<KVT, RT>::NST;
+    constexpr bool QLDS = RT > 1;
+    constexpr bool PRIO = DecLds<KVT, RT, WGW, WPE>::PRIO;
+    auto& s_u = s.u;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
-    const int g = blockIdx.y, rec = blockIdx.x;
     const int kmax = pos0 + nq - 1;
     const int nchunk = kmax / CHUNK + 1;
     const int cls = rec * WGW + wave;
@@ -491,6 +499,28 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     }
     TRACE(4);
     prof_end(prof);
+}
+
+template <int KVT, int RT, int WGW, int WPE = 2>
+__global__ void __launch_bounds__(64 * WGW) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
+      unsigned long long* prof) {
+    __shared__ __attribute__((aligned(16))) DecLds<KVT, RT, WGW, WPE> s;
+    dec_body<KVT, RT, WGW, WPE>(s, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, prof);
+}
+
+// The two passes of a three-tile verify in one launch, grid (records, NKV, 2): z = 0 takes row tiles rt0 and rt0 + 1,
+// z = 1 tile rt0 + 2 (as k_dec4_3).
+template <int KVT, int WGW>
+__global__ void __launch_bounds__(64 * WGW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_dec_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
+        unsigned long long* prof) {
+    __shared__ __attribute__((aligned(16))) union {
+        DecLds<KVT, 2, WGW, 2> two;
+        DecLds<KVT, 1, WGW, 2> one;
+    } s;
+    if (blockIdx.z == 0) dec_body<KVT, 2, WGW, 2>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, prof);
+    else dec_body<KVT, 1, WGW, 2>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, prof);
 }
 
 // ---------------------------------------------------------------------------------------------- Q4_0 decode
@@ -1033,19 +1063,21 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
 // workgroup finishes alone at one wave per SIMD)
 constexpr int Q4_WGW = WG_CLASSES;
 constexpr int DEC_WGW = WG_CLASSES;
-#ifndef QWA_Q4_ONE_LAUNCH
-#define QWA_Q4_ONE_LAUNCH 1
+#ifndef QWA_ONE_LAUNCH
+#define QWA_ONE_LAUNCH 1
 #endif
-// 6..8-query Q4_0 verify: both passes (two tiles, one tile) as one launch
-constexpr bool Q4_ONE_LAUNCH = QWA_Q4_ONE_LAUNCH != 0;
+// 6..8-query verify in two passes (two tiles, one tile): both as one launch
+constexpr bool ONE_LAUNCH = QWA_ONE_LAUNCH != 0;
 #ifndef QWA_DEC3
 #define QWA_DEC3 1
 #endif
-// Three row tiles (6..8 queries) in one pass at one wave per SIMD.  F16 at every context (7 queries, one pass / two
-// passes: 25.4 / 30.3 us per layer at 4096 positions, 48.7 / 47.8 at 16384, 63.5 / 67.9 at 32768, 88.5 / 109.7 at
-// 65536).  Q8_0, whose int8 conversion hides behind a second wave in the two-tile pass, only below 8192 and from
-// 98304 positions on (19.4 / 27.0 at 4096, 41.2 / 36.6 at 16384, 53.8 / 51.4 at 32768, 65.6 / 61.7 at 49152,
-// 77.0 / 77.1 at 65536, 139 / 149 at 150000).  Q4_0 keeps two passes.
+// Three row tiles (6..8 queries) in one pass at one wave per SIMD, against the two passes (two tiles, one tile) as
+// one launch; 7 queries, us per layer, one pass / two passes:
+//   F16  (from 32768 positions on):  24.4 / 20.3 at 4096, 46.4 / 45.0 at 16384, 85.9 / 107.1 at 65536,
+//                                    150 / 230 at 150000
+//   Q8_0 (from 131072 positions on): 23.1 / 19.4 at 4096, 43.5 / 34.7 at 16384, 81.5 / 74.6 at 65536,
+//                                    107.2 / 100.2 at 100000, 145.2 / 148.8-155.7 at 150000
+// (Q8_0's int8 conversion hides behind the second wave of the two-tile pass.)  Q4_0 keeps two passes.
 constexpr bool PF3_VERIFY = QWA_DEC3 != 0;
 
 // The one-pass three-tile verify kernel where it is used (F16 or Q8_0, 6..8 queries); false if the call takes the
@@ -1068,17 +1100,20 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
                            float* work, hipStream_t st) {
     const int rt = (GRP * nq + 15) / 16;
     const dim3 grid(nrec, NKV);
+    // two row tiles share one pass over the cache; a third tile (6..8 queries) gets a pass of its own, in the same
+    // launch, unless the one-pass three-tile kernel takes the call
+    if (ONE_LAUNCH && rt == 3 && !three) {
+        unsigned long long* prof = profile_slot(2 * nrec * NKV, st);
+        if constexpr (KVT == QWA_KV_Q4_0)
+            hipLaunchKernelGGL((k_dec4_3<Q4_WGW>), dim3(nrec, NKV, 2), dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, 0,
+                               work, prof);
+        else
+            hipLaunchKernelGGL((k_dec_3<KVT, DEC_WGW>), dim3(nrec, NKV, 2), dim3(64 * DEC_WGW), 0, st, q, kv, pos0, nq,
+                               0, work, prof);
+        profile_launched(prof, st);
+        return;
+    }
     for (int t = 0; t < rt; t++) {
-        if constexpr (KVT == QWA_KV_Q4_0) {
-            // two row tiles share one pass over the cache; a third tile gets a pass of its own, in the same launch
-            if (Q4_ONE_LAUNCH && t == 0 && rt == 3) {
-                unsigned long long* prof = profile_slot(2 * nrec * NKV, st);
-                hipLaunchKernelGGL((k_dec4_3<Q4_WGW>), dim3(nrec, NKV, 2), dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq,
-                                   0, work, prof);
-                profile_launched(prof, st);
-                break;
-            }
-        }
         unsigned long long* prof = profile_slot((three ? 2 : 1) * nrec * NKV, st);  // three: 2 nrec half records
         if constexpr (KVT == QWA_KV_Q4_0) {
             if (t + 1 < rt) {
@@ -1113,7 +1148,7 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     // 6..8 queries: the one-pass three-tile kernel where it is the faster path (every path gives the same bits)
     const int npos = pos0 + nq;
     const bool three = PF3_VERIFY && (GRP * nq + 15) / 16 == 3 &&
-                       (kvt == QWA_KV_F16 || (kvt == QWA_KV_Q8_0 && (npos < 8192 || npos >= 98304)));
+                       ((kvt == QWA_KV_F16 && npos >= 32768) || (kvt == QWA_KV_Q8_0 && npos >= 131072));
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, three, w, st);
     else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, three, w, st);
     else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, false, w, st);
