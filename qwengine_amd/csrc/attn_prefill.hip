@@ -63,9 +63,10 @@ constexpr float PF_LOG2E = 1.4426950408889634f;
 constexpr float PF_RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maximum (natural-log units)
 
 // Partial softmax states of one pass live in the caller's workspace: per split and output row
-// (row = token * NH + head, ps rows per split) O / l as fp32 [split][row][HD] and (m, l) as fp32 [split][row]; the
-// combine reweights them by l * exp(m - M).  (fp16 partials would halve these bytes but add a third fp16 rounding,
-// up to 2^-12 |O|, on top of the fp16 P and output of the reference's own MMA kernel.)
+// (row = token * NH + head, ps rows per split) O / l as 24-bit floats [split][row][HD] (pack24x4: fp32 rounded to
+// 15 mantissa bits, relative error <= 2^-16) and (m, l) as fp32 [split][row]; the combine reweights them by
+// l * exp(m - M).  (fp16 partials would halve the fp32 bytes but add a third fp16 rounding, up to 2^-12 |O|, on top
+// of the fp16 P and output of the reference's own MMA kernel: measured above the tolerance.)
 
 // raw bytes of one tile in LDS, in the cache's own layout: K rows, V rows, K scales, V scales (8 fp16 per row)
 template <int KVT> struct PfRaw {
@@ -317,6 +318,18 @@ __device__ __forceinline__ float rows_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Partial O / l values are stored as the top 24 bits of their fp32 pattern (sign, exponent, 15 mantissa bits),
+// rounded to nearest: 3 bytes per value, relative error <= 2^-16.  Four values pack into three dwords.
+__device__ __forceinline__ uint3 pack24x4(float a, float b, float c, float d) {
+    const uint32_t t0 = (__float_as_uint(a) + 0x80u) >> 8, t1 = (__float_as_uint(b) + 0x80u) >> 8;
+    const uint32_t t2 = (__float_as_uint(c) + 0x80u) >> 8, t3 = (__float_as_uint(d) + 0x80u) >> 8;
+    return make_uint3(t0 | (t1 << 24), (t1 >> 8) | (t2 << 16), (t2 >> 16) | (t3 << 8));
+}
+__device__ __forceinline__ float4 unpack24x4(uint3 w) {
+    return make_float4(__uint_as_float(w.x << 8), __uint_as_float(((w.x >> 24) << 8) | ((w.y & 0xFFFFu) << 16)),
+                       __uint_as_float(((w.y >> 16) << 8) | ((w.z & 0xFFu) << 24)), __uint_as_float(w.z & 0xFFFFFF00u));
+}
+
 // One split of one row block: grid (row blocks, NKV, PF_NS).  Tokens 0 .. B-1 of this pass sit at cache positions
 // p0 .. p0 + B - 1.
 // IMG: tiles come as fp16 images (k_pf_image) of img_tiles tiles per KV head, copied straight into LDS; otherwise as
@@ -324,7 +337,7 @@ __device__ __forceinline__ float rows_sum(float x) {
 template <int KVT, bool IMG>
 __global__ void __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(PF_WPE, PF_WPE)))
 k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uint8_t* __restrict__ img, int img_tiles,
-          float4* __restrict__ part_o, float2* __restrict__ part_ml, int ps, unsigned long long* prof) {
+          uint3* __restrict__ part_o, float2* __restrict__ part_ml, int ps, unsigned long long* prof) {
     prof_start(prof);
     using L = PfRaw<KVT>;
     constexpr int NBUF = IMG ? PF_IMG_NBUF : L::NBUF;
@@ -580,10 +593,10 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
         const size_t prow = (size_t)sp * ps + rr;
         if (lg == 0) part_ml[prow] = make_float2(m[rt], lt);
         const float il = lt > 0.0f ? 1.0f / lt : 0.0f;  // a split that saw no key leaves l = 0 and O = 0
-        float4* dst = part_o + prow * (HD / 4) + lg;
+        uint3* dst = part_o + prow * (HD / 4) + lg;
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
-            dst[4 * dt] = make_float4(o[rt][dt][0] * il, o[rt][dt][1] * il, o[rt][dt][2] * il, o[rt][dt][3] * il);
+            dst[4 * dt] = pack24x4(o[rt][dt][0] * il, o[rt][dt][1] * il, o[rt][dt][2] * il, o[rt][dt][3] * il);
     }
     prof_end(prof);
 }
@@ -592,7 +605,7 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
 // wave per row (token * NH + head), 4 dims per lane.  Split s weighs w_s = l_s exp(m_s - M); the row's output is
 // sum_s w_s (O_s / l_s) / sum_s w_s.
 __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ gate, int nrows,
-                                                    const float4* __restrict__ part_o,
+                                                    const uint3* __restrict__ part_o,
                                                     const float2* __restrict__ part_ml, int ps,
                                                     uint16_t* __restrict__ out16) {
     const int rr = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -603,7 +616,7 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ ga
 #pragma unroll
     for (int s = 0; s < PF_NS; s++) {
         ml[s] = part_ml[(size_t)s * ps + rr];
-        ov[s] = part_o[((size_t)s * ps + rr) * (HD / 4) + lane];
+        ov[s] = unpack24x4(part_o[((size_t)s * ps + rr) * (HD / 4) + lane]);
         mx = fmaxf(mx, ml[s].x);
     }
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -630,7 +643,7 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ ga
 struct PfWork {
     uint8_t* img;
     float2* ml;
-    float4* o;
+    uint3* o;  // 24-bit values, 4 per uint3
     int tiles, ps;
     size_t bytes;
 };
@@ -643,10 +656,10 @@ static PfWork pf_work_layout(uint8_t* base, int B, int n_pos) {
     w.ps = NH * min(B, PF_MAXB);
     const size_t img = PF_IMAGE ? align256((size_t)NKV * w.tiles * PF_IMG_BYTES) : 0;
     const size_t ml = align256((size_t)PF_NS * w.ps * sizeof(float2));
-    const size_t o = (size_t)PF_NS * w.ps * HD * sizeof(float);
+    const size_t o = (size_t)PF_NS * w.ps * HD * 3;
     w.img = base;
     w.ml = reinterpret_cast<float2*>(base + img);
-    w.o = reinterpret_cast<float4*>(base + img + ml);
+    w.o = reinterpret_cast<uint3*>(base + img + ml);
     w.bytes = img + ml + o;
     return w;
 }
