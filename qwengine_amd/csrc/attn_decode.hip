@@ -46,6 +46,10 @@ static __device__ unsigned long long dec_trace[4096][8];
 
 constexpr int REC = 260;    // partial record: m, l, 2 pad, O[256] (16-byte aligned O)
 constexpr int CGRP = 16;    // combine: records per fixed summation group
+#ifndef QWA_DEC_INTERLEAVE
+#define QWA_DEC_INTERLEAVE 1
+#endif
+constexpr bool DEC_INTERLEAVE = QWA_DEC_INTERLEAVE != 0;  // classes spread over the records (see dec_body)
 constexpr int CHUNK = 16;   // keys per chunk
 constexpr int WG_CLASSES = 8;                   // classes (waves) per decode workgroup, every format
 constexpr int NREC = DEC_CLASSES / WG_CLASSES;  // records (workgroups) per KV head
@@ -309,7 +313,12 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
     const int i16 = lane & 15, lg = lane >> 4;
     const int kmax = pos0 + nq - 1;
     const int nchunk = kmax / CHUNK + 1;
-    const int cls = rec * WGW + wave;
+    // record r holds classes r, r + R, ..., r + 7 R (R = DEC_CLASSES / WG_CLASSES records), so the classes with one
+    // chunk more than the others are spread over the records; a 4-wave workgroup (half records) takes classes
+    // r + R (4 h + w) of half h = rec & 1 of record r = rec >> 1
+    constexpr int R = DEC_CLASSES / WG_CLASSES;
+    const int cls = !DEC_INTERLEAVE ? rec * WGW + wave
+                    : WGW == WG_CLASSES ? rec + R * wave : (rec >> 1) + R * (WGW * (rec & 1) + wave);
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;  // chunks of this wave
     const size_t rowbase = (size_t)g * kv.capacity;
 
@@ -357,7 +366,7 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
 
     if (nmine > 0) {
         for (int j = 0; j < nmine; j++) {
-            if constexpr (PRIO) pair_priority<WGW>(s_u.a.prog, wave, lane, j);
+            if constexpr (PRIO) pair_priority<WGW>(s_u.a.prog, wave, lane, DEC_INTERLEAVE ? j - nmine : j);
             const int slot = j % NST;
             const int kb = chunk_key(j);
             wait_vmcnt<C::NLOAD * (NST - 1)>();  // this slot has landed; the later ones may still fly
@@ -645,7 +654,8 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
     const int i16 = lane & 15, lg = lane >> 4;
     const int kmax = pos0 + nq - 1;
     const int nchunk = kmax / CHUNK + 1;
-    const int cls = rec * WGW + wave;
+    // record rec holds classes rec, rec + R, ..., rec + 7 R (as dec_body)
+    const int cls = DEC_INTERLEAVE ? rec + (DEC_CLASSES / WGW) * wave : rec * WGW + wave;
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;
     const size_t rowbase = (size_t)g * kv.capacity;
 
@@ -837,7 +847,7 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
                 if (NST < nmine) issue(NST);
             }
             for (int j = 0; j + 1 < nmine; j++) {
-                pair_priority<WGW>(s_prog, wave, lane, j);
+                pair_priority<WGW>(s_prog, wave, lane, DEC_INTERLEAVE ? j - nmine : j);
 #ifdef QWA_TRACE
                 tw = __builtin_amdgcn_s_memtime();
 #endif
@@ -867,7 +877,7 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
 #endif
         } else {
             for (int j = 0; j < nmine; j++) {
-                pair_priority<WGW>(s_prog, wave, lane, j);
+                pair_priority<WGW>(s_prog, wave, lane, DEC_INTERLEAVE ? j - nmine : j);
                 if (j + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
                 else wait_vmcnt<0>();
                 // two row tiles: V is read after the softmax, so K and V registers are never live together
@@ -1143,7 +1153,9 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     // one record per workgroup; workgroups past the last chunk would hold no class with a chunk
     const int nchunk = (pos0 + nq - 1) / CHUNK + 1;
     const int wgw = kvt == QWA_KV_Q4_0 ? Q4_WGW : DEC_WGW;
-    const int nsplit = min(DEC_CLASSES / wgw, (nchunk + wgw - 1) / wgw);
+    // records launched: every class with a chunk must belong to one (interleaved records hold classes r + 64 w)
+    const int nsplit =
+        DEC_INTERLEAVE ? min(DEC_CLASSES / wgw, nchunk) : min(DEC_CLASSES / wgw, (nchunk + wgw - 1) / wgw);
     float* w = static_cast<float*>(work);
     // 6..8 queries: the one-pass three-tile kernel where it is the faster path (every path gives the same bits)
     const int npos = pos0 + nq;
