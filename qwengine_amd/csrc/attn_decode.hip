@@ -454,8 +454,10 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
             VRaw<KVT> vr[4];
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) v_raw<KVT>(vr[jj], vst, vsc, 4 * lg + jj, i16);
-            __builtin_amdgcn_wave_barrier();
-            // the slot is consumed: refill it with the chunk NST ahead (clamped: re-reads cached lines at the end)
+            // the slot is consumed once these reads have returned: the refill's direct-to-LDS writes must not land
+            // before them (a refill served from L2 returns within a few hundred cycles)
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            // refill the slot with the chunk NST ahead (clamped: re-reads cached lines at the end)
             issue(ring[slot], chunk_key(j + NST));
             constexpr int NW = sizeof(vr[0].w) / 4;  // raw words per 16 dims
             constexpr int DPW = 16 / NW;             // dims per raw word
