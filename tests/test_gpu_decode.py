@@ -250,7 +250,7 @@ def test_verify_passes_long_context(gpu, oracle, kvt, nq, pos0):
         many = _decode(kv2, q2, g2, 30000, nq).cpu().numpy()
         one = _decode(kv2, q2[nq - 1:].contiguous(), g2[nq - 1:].contiguous(), 30000 + nq - 1, 1).cpu().numpy()
         assert np.array_equal(many[nq - 1].view(np.uint32), one[0].view(np.uint32))
-    for t in (0, nq - 1):
+    for t in range(nq):
         one = _decode(kv, q[t:t + 1].contiguous(), gate[t:t + 1].contiguous(), pos0 + t, 1).cpu().numpy()
         assert np.array_equal(out[t].view(np.uint32), one[0].view(np.uint32)), t
 
