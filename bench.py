@@ -265,6 +265,20 @@ def main():
         extra["prefill_tflops"] = round(tflops, 1)
         extra["prefill_mfma_frac"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
         extra["prefill_kernel_mfma_frac"] = round(flop / (extra["prefill_kernel_ms"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+        del kv4
+        # the reference's own prefill bench points (tests/kernels/test_attn_prefill.cu:79-101): B = 512 chunks at
+        # p0 = 7680, 32256, 99488 over Q8_0, flop = 4 B 24 256 (p0 + B / 2) as it counts them
+        B = 512
+        kvr = fill_cache(ops, torch, ops.Q8_0, 99488 + B, 4100, 0.0)
+        ops.attn_prefill_reserve(B, 99488 + B)
+        for p0 in (7680, 32256, 99488):
+            time_calls(torch, lambda: ops.attn_prefill(qp[:B], gp[:B], kvr, ops.Q8_0, B, p0, o16[:B]), 1, 2)
+            ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp[:B], gp[:B], kvr, ops.Q8_0, B, p0, o16[:B]),
+                                   5, 0) for _ in range(4))[1:3]
+            ms = sum(ms) / 2
+            extra[f"prefill_512_at_{p0}_ms"] = round(ms, 4)
+            extra[f"prefill_512_at_{p0}_tflops"] = round(4.0 * B * 24 * 256 * (p0 + B / 2) / (ms * 1e-3) / 1e12, 1)
+        del kvr
         extra.update(deltanet_extras(ops, torch, args.steps))
         extra.update(consumer_extras(ops, torch, args.steps))
         result["extra"] = extra

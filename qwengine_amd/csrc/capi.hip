@@ -259,13 +259,18 @@ int qwa_attn_prefill_reserve(int max_B, int max_pos, void* stream) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return from_hip(e, fn);
-    // the workspace covers every call with B <= max_B and p0 + B <= max_pos (its size grows with both)
-    const size_t need = qwa::prefill_work_bytes(max_B, max_pos);
     std::lock_guard<std::mutex> lock(g_pf_mu);
     PfReservation* r = pf_find(dev, stream);
+    // the workspace covers every call with B <= max_B and p0 + B <= max_pos (its size grows with both); a second
+    // reservation on the stream widens the first, so the size is that of both maxima together
+    if (r != nullptr) {
+        max_B = std::max(r->max_B, max_B);
+        max_pos = std::max(r->max_pos, max_pos);
+    }
+    const size_t need = qwa::prefill_work_bytes(max_B, max_pos);
     if (r != nullptr && r->bytes >= need) {
-        r->max_B = std::max(r->max_B, max_B);
-        r->max_pos = std::max(r->max_pos, max_pos);
+        r->max_B = max_B;
+        r->max_pos = max_pos;
         return QWA_OK;
     }
     void* p = nullptr;
@@ -317,7 +322,7 @@ int qwa_attn_prefill(const float* q, const float* gate, const qwa_kv_layer* kv, 
         if (r == nullptr)
             return fail(QWA_ERR_RANGE, "%s: no workspace reserved for this stream on device %d "
                                        "(call qwa_attn_prefill_reserve at set-up)", fn, dev);
-        if (B > r->max_B || p0 + B > r->max_pos)
+        if (B > r->max_B || p0 + B > r->max_pos || qwa::prefill_work_bytes(B, p0 + B) > r->bytes)
             return fail(QWA_ERR_RANGE, "%s: B = %d, p0 + B = %d beyond the stream's reservation (max_B %d, max_pos %d)",
                         fn, B, p0 + B, r->max_B, r->max_pos);
         work = r->ptr;

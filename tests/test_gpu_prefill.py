@@ -139,6 +139,25 @@ def test_prefill_without_reservation_is_refused(gpu):
     ops.attn_prefill_release(stream=s)
 
 
+def test_prefill_reservations_widen(gpu):
+    """Two reservations on one stream cover both maxima together: after (B 64, 300 positions) and (B 8, 2100
+    positions) a call with B = 64 ending at 2100 runs in a workspace sized for both, with the caller-workspace bits."""
+    kvt, p0, B = ops.Q8_0, 2036, 64
+    kv, q, gate = _inputs(kvt, p0, B, 85)
+    s = torch.cuda.Stream()
+    out = torch.empty((B, 24, 256), dtype=torch.float16, device="cuda")
+    ops.attn_prefill_reserve(64, 300, stream=s)
+    ops.attn_prefill_reserve(8, 2100, stream=s)
+    ops.attn_prefill(q, gate, kv, kvt, B, p0, out, stream=s)
+    s.synchronize()
+    work = torch.empty(ops.attn_prefill_work_bytes(B, p0 + B), dtype=torch.uint8, device="cuda")
+    want = torch.empty_like(out)
+    ops.attn_prefill_ws(q, gate, kv, kvt, B, p0, want, work)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    ops.attn_prefill_release(stream=s)
+
+
 def test_prefill_in_hip_graph(gpu):
     """The drop-in call captured into a HIP graph on its first use (the workspace is reserved beforehand, nothing
     is allocated inside the call): every replay, with eager prefills of other inputs in between, equals the eager
