@@ -14,8 +14,8 @@
 //    LDS instead and all threads dequantise the next tile cooperatively inside the loop;
 //  * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16 (fp32 accumulation); P^T comes out of the S^T
 //    accumulator already in B-operand layout; online softmax in fp32 with a lazy rescale;
-//  * the causal key range of a row block is cut into PF_NS fixed splits (one workgroup each) so that the
-//    96 row blocks x 4 KV heads of a 1024-token chunk fill the chip; each split leaves a partial state (m, l, O / l)
+//  * the causal key range of a row block is cut into fixed splits (pf_splits, one workgroup each) so that the
+//    24 row blocks x 4 KV heads of a 1024-token chunk fill the chip; each split leaves a partial state (m, l, O / l)
 //    in the caller's workspace and k_pf_combine merges the splits in a fixed order, applies the sigmoid gate and
 //    writes fp16.  Chunks longer than PF_MAXB tokens run as several passes.  Nothing here allocates: the images
 //    and partial states live in a workspace of prefill_work_bytes(B, p0 + B) bytes.
@@ -45,6 +45,20 @@ constexpr int PF_KT = PF_TILE / 16;              // 16-key MFMA tiles per tile
 constexpr int PF_NS = PF_ROWS == 192 ? 6 : 8;    // key-range splits per row block (3 rounds of the chip for B = 1024)
 constexpr int PF_MAXB = 1024;                    // tokens per pass
 constexpr int PF_MAXROWS = PF_MAXB * NH;         // output rows per pass
+#ifndef QWA_PF_FILL
+#define QWA_PF_FILL 1
+#endif
+// splits of a pass of nb tokens (at most PF_NS): the count that fills the chip's 256 CUs in whole rounds best, i.e.
+// the fewest rounds per split, ceil(workgroups / 256) / splits (1024 tokens: 8 splits, 3 rounds; 512 tokens: 5
+// splits, one round of 240 workgroups, where 8 would make 1.5 rounds)
+inline int pf_splits(int nb) {
+    if (!QWA_PF_FILL) return PF_NS;
+    const int groups = (GRP * nb + PF_ROWS - 1) / PF_ROWS * NKV;
+    int best = PF_NS;
+    for (int ns = PF_NS - 1; ns >= 5; ns--)  // 5 .. PF_NS: the instantiated kernels
+        if ((long)((groups * ns + 255) / 256) * best < (long)((groups * best + 255) / 256) * ns) best = ns;
+    return best;
+}
 constexpr int KS_LD = HD + 8;                    // K tile row stride (halves)
 constexpr int VT_LD = PF_TILE + 8;               // V^T tile row stride (halves)
 #ifndef QWA_PF_VD
@@ -330,11 +344,11 @@ __device__ __forceinline__ float4 unpack24x4(uint3 w) {
                        __uint_as_float(((w.y >> 16) << 8) | ((w.z & 0xFFu) << 24)), __uint_as_float(w.z & 0xFFFFFF00u));
 }
 
-// One split of one row block: grid (row blocks, NKV, PF_NS).  Tokens 0 .. B-1 of this pass sit at cache positions
+// One split of one row block: grid (row blocks, NKV, NS splits).  Tokens 0 .. B-1 of this pass sit at cache positions
 // p0 .. p0 + B - 1.
 // IMG: tiles come as fp16 images (k_pf_image) of img_tiles tiles per KV head, copied straight into LDS; otherwise as
 // raw quantized bytes dequantised in the loop.
-template <int KVT, bool IMG>
+template <int KVT, bool IMG, int NS>
 __global__ void __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(PF_WPE, PF_WPE)))
 k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uint8_t* __restrict__ img, int img_tiles,
           uint3* __restrict__ part_o, float2* __restrict__ part_ml, int ps, unsigned long long* prof) {
@@ -350,11 +364,16 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
 #if QWA_PF_XCD
     // XCD-aware numbering: workgroup lin is dispatched to XCD lin % 8; give each XCD whole (KV head, split) pairs, so
     // the row blocks that read the same image tiles share one L2
-    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const int xcd = lin & 7, slot = lin >> 3, nrb = gridDim.x;
-    static_assert(NKV * PF_NS % 8 == 0, "whole (KV head, split) pairs per XCD");
-    const int pair = NKV * PF_NS / 8 * xcd + slot / nrb;
-    const int bx = slot % nrb, g = pair % NKV, sp = pair / NKV;
+    // (a split count with NKV x NS not a multiple of 8 keeps the plain numbering)
+    int bx = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
+    if constexpr ((NKV * NS) % 8 == 0) {
+        const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int xcd = lin & 7, slot = lin >> 3, nrb = gridDim.x;
+        const int pair = NKV * NS / 8 * xcd + slot / nrb;
+        bx = slot % nrb;
+        g = pair % NKV;
+        sp = pair / NKV;
+    }
 #else
     const int bx = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
 #endif
@@ -364,7 +383,7 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
     const int last_row = min(row0 + PF_ROWS, nrows) - 1;
     const int kmax = p0 + last_row / GRP;
     const int n_tiles = kmax / PF_TILE + 1;
-    const int tb = sp * n_tiles / PF_NS, nt = (sp + 1) * n_tiles / PF_NS - tb;
+    const int tb = sp * n_tiles / NS, nt = (sp + 1) * n_tiles / NS - tb;
     const size_t rowbase = (size_t)g * kv.capacity;
     const int nvm = IMG ? PF_IMG_BYTES / 1024 / PF_WAVES : L::count(wave);
     uint32_t raw_lds[NBUF];
@@ -601,20 +620,21 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
     prof_end(prof);
 }
 
-// Merges the PF_NS partial states of each output row in split order, applies the sigmoid gate and writes fp16: one
+// Merges the partial states of the ns splits of each output row in split order, applies the sigmoid gate and writes fp16: one
 // wave per row (token * NH + head), 4 dims per lane.  Split s weighs w_s = l_s exp(m_s - M); the row's output is
 // sum_s w_s (O_s / l_s) / sum_s w_s.
+template <int NS>
 __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ gate, int nrows,
                                                     const uint3* __restrict__ part_o,
                                                     const float2* __restrict__ part_ml, int ps,
                                                     uint16_t* __restrict__ out16) {
     const int rr = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (rr >= nrows) return;
-    float2 ml[PF_NS];
-    float4 ov[PF_NS];
+    float2 ml[NS];
+    float4 ov[NS];
     float mx = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < PF_NS; s++) {
+    for (int s = 0; s < NS; s++) {
         ml[s] = part_ml[(size_t)s * ps + rr];
         ov[s] = unpack24x4(part_o[((size_t)s * ps + rr) * (HD / 4) + lane]);
         mx = fmaxf(mx, ml[s].x);
@@ -622,7 +642,7 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ ga
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float wsum = 0.0f;
 #pragma unroll
-    for (int s = 0; s < PF_NS; s++) {
+    for (int s = 0; s < NS; s++) {
         const float w = ml[s].x == -INFINITY ? 0.0f : fast_exp2((ml[s].x - mx) * PF_LOG2E) * ml[s].y;
         acc.x += w * ov[s].x;
         acc.y += w * ov[s].y;
@@ -639,7 +659,8 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ ga
 }
 
 // Workspace layout of one call: the fp16 images of the KV range [0, p0 + B) (NKV x tiles x 32 KB; none when built
-// without images), then the (m, l) pairs and the partial O of one pass (PF_NS x ps rows, ps = NH x min(B, PF_MAXB)).
+// without images), then the (m, l) pairs and the partial O of one pass (up to PF_NS x ps rows, ps = NH x min(B,
+// PF_MAXB)).
 struct PfWork {
     uint8_t* img;
     float2* ml;
@@ -669,10 +690,17 @@ size_t prefill_work_bytes(int B, int n_pos) { return pf_work_layout(nullptr, B, 
 template <int KVT>
 static void launch_prefill_pass(const float* qp, const qwa_kv_layer& kv, int nb, int p0, const PfWork& w,
                                 hipStream_t st) {
-    const dim3 grid((GRP * nb + PF_ROWS - 1) / PF_ROWS, NKV, PF_NS);
+    const int ns = pf_splits(nb);
+    const dim3 grid((GRP * nb + PF_ROWS - 1) / PF_ROWS, NKV, ns);
     unsigned long long* prof = profile_slot(grid.x * grid.y * grid.z, st);
-    hipLaunchKernelGGL((k_prefill<KVT, PF_IMAGE>), grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0, w.img, w.tiles, w.o,
-                       w.ml, w.ps, prof);
+#define QWA_PF_LAUNCH(N)                                                                                            \
+    hipLaunchKernelGGL((k_prefill<KVT, PF_IMAGE, N>), grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0, w.img, w.tiles, \
+                       w.o, w.ml, w.ps, prof)
+    if (ns == 5) QWA_PF_LAUNCH(5);
+    else if (ns == 6) QWA_PF_LAUNCH(6);
+    else if (ns == 7) QWA_PF_LAUNCH(7);
+    else QWA_PF_LAUNCH(PF_NS);
+#undef QWA_PF_LAUNCH
     profile_launched(prof, st);
 }
 
@@ -695,8 +723,16 @@ hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer&
         else if (kvt == QWA_KV_Q8_0) launch_prefill_pass<QWA_KV_Q8_0>(qp, kv, nb, p0 + t0, w, st);
         else launch_prefill_pass<QWA_KV_Q4_0>(qp, kv, nb, p0 + t0, w, st);
         const int nrows = nb * NH;
-        hipLaunchKernelGGL(k_pf_combine, dim3((nrows + 3) / 4), dim3(256), 0, st, gate + (size_t)t0 * NH * HD, nrows,
-                           w.o, w.ml, w.ps, out16 + (size_t)t0 * NH * HD);
+        const float* gp = gate + (size_t)t0 * NH * HD;
+        uint16_t* op = out16 + (size_t)t0 * NH * HD;
+        const dim3 cg((nrows + 3) / 4), cb(256);
+        switch (pf_splits(nb)) {
+#define QWA_PF_COMBINE(N) \
+    case N: hipLaunchKernelGGL(k_pf_combine<N>, cg, cb, 0, st, gp, nrows, w.o, w.ml, w.ps, op); break
+            QWA_PF_COMBINE(5); QWA_PF_COMBINE(6); QWA_PF_COMBINE(7);
+            default: hipLaunchKernelGGL(k_pf_combine<PF_NS>, cg, cb, 0, st, gp, nrows, w.o, w.ml, w.ps, op); break;
+#undef QWA_PF_COMBINE
+        }
     }
     return hipGetLastError();
 }
