@@ -1,7 +1,8 @@
 """GPU parity of causal prefill attention (fp16 MFMA kernel) against the float64 oracle on the stored cache, and
 against the FP32 test kernel at the reference's chunk cases (tests/kernels/test_attn_prefill.cu:20-72: a cache of
 1500 positions filled through rope_table + attn_prep_rows, chunks (p0, B) in {(0,37), (0,512), (300,129),
-(1000,500), (1480,20)}), plus a 1300-token chunk (two passes of the kernel's 1024-token limit), long-context chunks
+(1000,500), (1480,20)}), plus a 1300-token chunk (two passes of the kernel's 1024-token limit), chunks of 420 and 360
+tokens (the kernel cuts their key ranges into 6 and 7 splits; 500 and 512 take 5, the rest 8), long-context chunks
 of every format, the BASELINE 1024-token chunk at p0 = 32768 on all of its queries, and the ownership contract of
 the workspace: the caller-owned form gives the drop-in call's bits, a captured HIP graph replays correctly, two
 streams with their own workspaces do not interfere, and a stream without a reservation is refused."""
@@ -14,7 +15,7 @@ from kvutil import KVTS, KV_NAMES, assert_close, dequant_cache, make_cache, seed
 
 pytestmark = pytest.mark.gpu
 
-CASES = [(0, 37), (0, 512), (300, 129), (1000, 500), (1480, 20), (200, 1300)]
+CASES = [(0, 37), (0, 512), (300, 129), (1000, 500), (1480, 20), (200, 1300), (0, 420), (1100, 360)]
 
 
 @pytest.fixture(scope="module", params=KVTS, ids=lambda k: KV_NAMES[k])
