@@ -5,8 +5,9 @@ Headline (BASELINE.json metric): decode attention over a 150000-position Q4_0 KV
 head_dim 256, one query per call.  One "step" = one token's decode attention over all 16 attention layers of the
 model, each layer with its own cache (16 x 172.8 MB, so consecutive calls cannot be served from the 256 MB
 Infinity Cache).  value = algorithmic HBM bytes (150000 x 1152 B per layer) / time per layer, in GB/s.
-Secondary figures in the same line: 7-query verify at 150000 and 32768 positions, Q8_0 decode with append at 4096,
-and the 1024-token prefill chunk at p0 = 32768 (TFLOP/s against the fp16 MFMA dense peak).
+Secondary figures in the same line: 7-query verify at 150000 and 32768 positions, F16 decode at 4096 (C1), Q8_0
+decode with append at 4096, and the 1024-token prefill chunk at p0 = 32768 (TFLOP/s against the fp16 MFMA dense
+peak).
 
 The CPU baseline (rank 0, N = 1 only) is the oracle's restatement of the reference CPU attention
 (src/reference/ref_model.cpp:138-163: fp32 8-lane FMA dots, double softmax, OpenMP over (token, head)) on bounded
@@ -227,6 +228,16 @@ def main():
                     (n + 7) * BYTES_PER_POS[kvo] / (us * 1e-6) / 1e9, 1)
             del lo
             torch.cuda.empty_cache()
+        # C1: F16 4096 decode, one query (the CPU-runnable case; 16 layers of 16.8 MB)
+        l1 = [fill_cache(ops, torch, ops.F16, 4097, 5000 + i, 0.0) for i in range(L)]
+        ms = time_calls(torch, lambda: [ops.attn_decode_multi(q, gate, kv, ops.F16, 4096, 1, work, out) for kv in l1],
+                        max(5, args.steps // 5), 2)
+        extra["decode_f16_4096_us_per_layer"] = round(ms * 1000.0 / L, 3)
+        ms = time_graph(torch, lambda: [ops.attn_decode_multi(q, gate, kv, ops.F16, 4096, 1, work, out) for kv in l1],
+                        max(5, args.steps // 5))
+        extra["decode_f16_4096_us_per_layer_graph"] = round(ms * 1000.0 / L, 3)
+        extra["decode_f16_4096_gbs_graph"] = round(4097 * 4096 / (ms * 1e-3 / L) / 1e9, 1)
+        del l1
         # C2: Q8_0 4096 decode with the new token's quantize-on-append (append + decode per layer)
         l2 = [fill_cache(ops, torch, ops.Q8_0, 4097, 3000 + i, 0.0) for i in range(L)]
         knew = torch.randn((1, 4, 256), device="cuda")
