@@ -85,28 +85,47 @@ __host__ __device__ constexpr int kpos(int row, int byte) {
 
 
 // Direct-to-LDS loads of one chunk (16 B per lane per instruction: K piece-major, V row-major, then the scales).
-// Rows past kmax re-read row kmax (no read outside the window; their scores are masked and their probabilities are
-// exact zeros).
+// A full chunk (every row inside the window) loads from wave-uniform bases (scalar registers) with per-lane offsets
+// fixed for the whole kernel: K piece 4 i + lane / 16 of row lane % 16 at koff + 64 i, V bytes 1024 i + 16 lane,
+// scales 4 lane.  The chunk holding key kmax takes per-lane addresses: rows past kmax re-read row kmax (no read
+// outside the window; their scores are masked and their probabilities are exact zeros).
+template <int KVT>
+__device__ __forceinline__ uint32_t chunk_koff(int lane) {
+    return (uint32_t)((lane & 15) * ChunkLds<KVT>::VB + 16 * (lane >> 4));
+}
+
 template <int KVT>
 __device__ __forceinline__ void issue_chunk(uint8_t* dst, const qwa_kv_layer& kv, size_t rowbase, int kb, int kmax,
-                                           int lane) {
+                                            int lane, uint32_t koff) {
     using C = ChunkLds<KVT>;
     constexpr int VB = C::VB;
+    const uint32_t d = lds_addr(dst);
+    if (kb + CHUNK - 1 <= kmax) {
+        const size_t row0 = rowbase + kb;
+        const uint8_t* kp = kv.k + row0 * VB;
+        const uint8_t* vp = kv.v + row0 * VB;
+#pragma unroll
+        for (int i = 0; i < C::NI; i++) {
+            dma_sv<16>(d + 1024 * i, kp + 64 * i, koff);
+            dma_sv<16>(d + C::KBYTES + 1024 * i, vp + 1024 * i, 16 * lane);
+        }
+        if constexpr (C::SC) {
+            dma_sv<4>(d + 2 * C::KBYTES, kv.ks + row0 * 8, 4 * lane);
+            dma_sv<4>(d + 2 * C::KBYTES + C::SC, kv.vs + row0 * 8, 4 * lane);
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < C::NI; i++) {
-        const int kn = lane & 15, kp = 4 * i + (lane >> 4);                 // K slot: piece kp of row kn
+        const int kn = lane & 15, kpc = 4 * i + (lane >> 4);               // K slot: piece kpc of row kn
         const int vn = (1024 * i + 16 * lane) / VB, vbyte = (1024 * i + 16 * lane) % VB;  // V: row-major
-        __builtin_amdgcn_global_load_lds(kv.k + (rowbase + min(kb + kn, kmax)) * VB + 16 * kp,
-                                         (lds_void*)(dst + 1024 * i), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(kv.v + (rowbase + min(kb + vn, kmax)) * VB + vbyte,
-                                         (lds_void*)(dst + C::KBYTES + 1024 * i), 16, 0, 0);
+        dma_v<16>(d + 1024 * i, kv.k + (rowbase + min(kb + kn, kmax)) * VB + 16 * kpc);
+        dma_v<16>(d + C::KBYTES + 1024 * i, kv.v + (rowbase + min(kb + vn, kmax)) * VB + vbyte);
     }
     if constexpr (C::SC) {
         const size_t row = rowbase + min(kb + lane / 4, kmax);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(kv.ks + row * 8) + 4 * (lane & 3),
-                                         (lds_void*)(dst + 2 * C::KBYTES), 4, 0, 0);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(kv.vs + row * 8) + 4 * (lane & 3),
-                                         (lds_void*)(dst + 2 * C::KBYTES + C::SC), 4, 0, 0);
+        dma_v<4>(d + 2 * C::KBYTES, reinterpret_cast<const uint8_t*>(kv.ks + row * 8) + 4 * (lane & 3));
+        dma_v<4>(d + 2 * C::KBYTES + C::SC, reinterpret_cast<const uint8_t*>(kv.vs + row * 8) + 4 * (lane & 3));
     }
 }
 
@@ -309,7 +328,7 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
     constexpr bool QLDS = RT > 1;
     constexpr bool PRIO = DecLds<KVT, RT, WGW, WPE>::PRIO;
     auto& s_u = s.u;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
     const int kmax = pos0 + nq - 1;
     const int nchunk = kmax / CHUNK + 1;
@@ -325,7 +344,8 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
     TRACE(0);
     uint8_t(*ring)[C::BYTES] = s_u.a.ring[wave];
     auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * min(j, nmine - 1)); };
-    auto issue = [&](uint8_t* dst, int kb) { issue_chunk<KVT>(dst, kv, rowbase, kb, kmax, lane); };
+    const uint32_t koff = chunk_koff<KVT>(lane);
+    auto issue = [&](uint8_t* dst, int kb) { issue_chunk<KVT>(dst, kv, rowbase, kb, kmax, lane, koff); };
     // the ring's loads go out before the Q set-up, so their HBM latency overlaps it
     if (nmine > 0) {
 #pragma unroll
