@@ -27,9 +27,10 @@ sys.path.insert(0, HERE)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 METRIC = "decode attn µs/layer + HBM GB/s @150K Q4_0 KV; prefill attn TFLOP/s (1024-tok chunk)"
-# HBM bytes per k_dec4 launch at the headline workload, measured with rocprofv3 PMC counters (read 173.1 MB + write
-# 1.6 MB; the kernel's algorithmic bytes are 172.8 MB)
-KDEC_TRAFFIC = 174.7e6
+# HBM bytes per k_dec4 launch at the headline workload come from the committed rocprofv3 PMC summary below.  It records
+# the digest of the decode kernel's sources it was measured on; a run on other sources reports traffic null.
+TRAFFIC_PROFILE = os.path.join("profiles", "decode_q4_0_150k_hbm_traffic.md")
+DECODE_SOURCES = ("attn_decode.hip", "kv_operands.hpp", "launch.hpp", "qwattn_common.hpp")
 BYTES_PER_POS = {0: 4096, 1: 2176, 2: 1152}  # K + V values and scales over the 4 KV heads
 
 
@@ -46,11 +47,42 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline decode only")
     ap.add_argument("--consumer-only", action="store_true",
                     help="print only the output-projection consumer figures (GEMV, fp16 GEMM)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="print only the prefill figures (C4 and the reference's 512-token points; for profiling)")
     ap.add_argument("--deltanet-only", action="store_true",
                     help="print only the Gated DeltaNet figures (for profiling those kernels)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run 5 device copies of 512 MiB (a known-size kernel to calibrate HBM counters)")
     return ap.parse_args()
+
+
+def decode_source_digest():
+    """sha256 (first 16 hex digits) over the decode kernel's source files, in DECODE_SOURCES order."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in DECODE_SOURCES:
+        with open(os.path.join(HERE, "qwengine_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic():
+    """(bytes per k_dec4 launch, note) from TRAFFIC_PROFILE's machine-readable line
+    `traffic: kernel=<name> source_digest=<hex> read_bytes=<R> write_bytes=<W>`; (None, why) when the summary is
+    missing or was measured on other decode sources than this tree's."""
+    import re
+    try:
+        with open(os.path.join(HERE, TRAFFIC_PROFILE)) as fh:
+            text = fh.read()
+    except OSError:
+        return None, f"{TRAFFIC_PROFILE} missing"
+    m = re.search(r"traffic: kernel=(\S+) source_digest=([0-9a-f]+) read_bytes=(\d+) write_bytes=(\d+)", text)
+    if not m:
+        return None, f"{TRAFFIC_PROFILE} has no traffic line"
+    if m.group(2) != decode_source_digest():
+        return None, f"{TRAFFIC_PROFILE} was measured on decode sources {m.group(2)}, this tree is " \
+                     f"{decode_source_digest()}: re-run its PMC commands"
+    return int(m.group(3)) + int(m.group(4)), f"{TRAFFIC_PROFILE} ({m.group(1)}, sources {m.group(2)})"
 
 
 def fill_cache(ops, torch, kvt, n, seed, outlier_frac=0.01):
@@ -115,6 +147,9 @@ def main():
     if args.consumer_only:
         print(json.dumps({"consumer": consumer_extras(ops, torch, args.steps)}), flush=True)
         return
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_extras(ops, torch)}), flush=True)
+        return
     n, L = args.positions, args.layers
     kvt = ops.Q4_0
     print(f"[bench] filling {L} layer caches of {n} Q4_0 positions", file=sys.stderr, flush=True)
@@ -160,6 +195,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     bytes_layer = n * BYTES_PER_POS[kvt]
+    traffic, traffic_note = measured_traffic() if (n, args.nq) == (150000, 1) else \
+        (None, "PMC traffic is measured for the headline workload only")
     gbs = bytes_layer / (us_layer * 1e-6) / 1e9
 
     result = {
@@ -175,16 +212,15 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (K/V ~N(0,1), 1% of key rows x8, quantized on append; random gate logits)",
-        "config": {"workload": "decode_q4_0_150k" if args.nq == 1 else f"verify{args.nq}_q4_0_150k", "kv": "q4_0",
+        "config": {"workload": ("decode" if args.nq == 1 else f"verify{args.nq}") + f"_q4_0_{n // 1000}k", "kv": "q4_0",
                    "positions": n, "queries_per_call": args.nq,
                    "layers_per_step": L, "q_heads": 24, "kv_heads": 4, "head_dim": 256},
         "decode_us_per_layer": round(us_layer, 3),
         "roofline": {"bound": "hbm", "achieved": round(bytes_layer / (kern_us * 1e-6) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(bytes_layer / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": KDEC_TRAFFIC if (n, L, args.nq) == (150000, 16, 1) else None,
-                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), calibrated on a "
-                                       "512 MiB copy, per k_dec4 dispatch",
+                     "traffic": traffic,
+                     "traffic_source": traffic_note,
                      "kernel": "k_dec4 (split-K Q4_0 decode), kernel time per call averaged over the timed calls",
                      "kernel_us": round(kern_us, 3), "launches": kern_n, "calls": calls,
                      "kernel_us_device_clock": round(kern_dev_us, 3),
@@ -252,44 +288,7 @@ def main():
         ms = time_graph(torch, c2, max(5, args.steps // 5))
         extra["decode_q8_4096_append_us_per_layer_graph"] = round(ms * 1000.0 / L, 3)
         del l2
-        # C4: prefill chunk of 1024 tokens at p0 = 32768, Q8_0
-        p0, B = 32768, 1024
-        kv4 = fill_cache(ops, torch, ops.Q8_0, p0 + B, 4000, 0.0)
-        qp = torch.randn((B, 24, 256), device="cuda").half().float()
-        gp = torch.randn((B, 24, 256), device="cuda")
-        o16 = torch.empty((B, 24, 256), dtype=torch.float16, device="cuda")
-        ops.attn_prefill_reserve(B, p0 + B)  # set-up: the stream's prefill workspace
-        # warm up, then the median of 4 groups of 5 calls
-        time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 1, 3)
-        ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 5, 0)
-                    for _ in range(4))[1:3]
-        ms = sum(ms) / 2
-        ops.profile_begin()
-        for _ in range(10):
-            ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16)
-        pk_ms, pk_n = ops.profile_end()
-        extra["prefill_kernel_ms"] = round(pk_ms / max(pk_n, 1), 4)
-        extra["prefill_kernel_ms_device_clock"] = round(ops.profile_device_ms() / max(pk_n, 1), 4)
-        flop = 4.0 * 24 * 256 * sum(p0 + t + 1 for t in range(B))
-        tflops = flop / (ms * 1e-3) / 1e12
-        extra["prefill_1024_at_32768_ms"] = round(ms, 4)
-        extra["prefill_tflops"] = round(tflops, 1)
-        extra["prefill_mfma_frac"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
-        extra["prefill_kernel_mfma_frac"] = round(flop / (extra["prefill_kernel_ms"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
-        del kv4
-        # the reference's own prefill bench points (tests/kernels/test_attn_prefill.cu:79-101): B = 512 chunks at
-        # p0 = 7680, 32256, 99488 over Q8_0, flop = 4 B 24 256 (p0 + B / 2) as it counts them
-        B = 512
-        kvr = fill_cache(ops, torch, ops.Q8_0, 99488 + B, 4100, 0.0)
-        ops.attn_prefill_reserve(B, 99488 + B)
-        for p0 in (7680, 32256, 99488):
-            time_calls(torch, lambda: ops.attn_prefill(qp[:B], gp[:B], kvr, ops.Q8_0, B, p0, o16[:B]), 1, 2)
-            ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp[:B], gp[:B], kvr, ops.Q8_0, B, p0, o16[:B]),
-                                   5, 0) for _ in range(4))[1:3]
-            ms = sum(ms) / 2
-            extra[f"prefill_512_at_{p0}_ms"] = round(ms, 4)
-            extra[f"prefill_512_at_{p0}_tflops"] = round(4.0 * B * 24 * 256 * (p0 + B / 2) / (ms * 1e-3) / 1e12, 1)
-        del kvr
+        extra.update(prefill_extras(ops, torch))
         extra.update(deltanet_extras(ops, torch, args.steps))
         extra.update(consumer_extras(ops, torch, args.steps))
         result["extra"] = extra
@@ -297,6 +296,51 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(ops, torch, n)
     print(json.dumps(result), flush=True)
+
+
+def prefill_extras(ops, torch):
+    """The 1024-token prefill chunk at p0 = 32768 over Q8_0 (C4; TFLOP/s against the fp16 MFMA dense peak, whole call
+    and the MFMA kernel alone) and the reference's own 512-token bench points."""
+    out = {}
+    # C4: prefill chunk of 1024 tokens at p0 = 32768, Q8_0
+    p0, B = 32768, 1024
+    kv4 = fill_cache(ops, torch, ops.Q8_0, p0 + B, 4000, 0.0)
+    qp = torch.randn((B, 24, 256), device="cuda").half().float()
+    gp = torch.randn((B, 24, 256), device="cuda")
+    o16 = torch.empty((B, 24, 256), dtype=torch.float16, device="cuda")
+    ops.attn_prefill_reserve(B, p0 + B)  # set-up: the stream's prefill workspace
+    # warm up, then the median of 4 groups of 5 calls
+    time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 1, 3)
+    ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 5, 0)
+                for _ in range(4))[1:3]
+    ms = sum(ms) / 2
+    ops.profile_begin()
+    for _ in range(10):
+        ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16)
+    pk_ms, pk_n = ops.profile_end()
+    out["prefill_kernel_ms"] = round(pk_ms / max(pk_n, 1), 4)
+    out["prefill_kernel_ms_device_clock"] = round(ops.profile_device_ms() / max(pk_n, 1), 4)
+    flop = 4.0 * 24 * 256 * sum(p0 + t + 1 for t in range(B))
+    tflops = flop / (ms * 1e-3) / 1e12
+    out["prefill_1024_at_32768_ms"] = round(ms, 4)
+    out["prefill_tflops"] = round(tflops, 1)
+    out["prefill_mfma_frac"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
+    out["prefill_kernel_mfma_frac"] = round(flop / (out["prefill_kernel_ms"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+    del kv4
+    # the reference's own prefill bench points (tests/kernels/test_attn_prefill.cu:79-101): B = 512 chunks at
+    # p0 = 7680, 32256, 99488 over Q8_0, flop = 4 B 24 256 (p0 + B / 2) as it counts them
+    B = 512
+    kvr = fill_cache(ops, torch, ops.Q8_0, 99488 + B, 4100, 0.0)
+    ops.attn_prefill_reserve(B, 99488 + B)
+    for p0 in (7680, 32256, 99488):
+        time_calls(torch, lambda: ops.attn_prefill(qp[:B], gp[:B], kvr, ops.Q8_0, B, p0, o16[:B]), 1, 2)
+        ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp[:B], gp[:B], kvr, ops.Q8_0, B, p0, o16[:B]),
+                               5, 0) for _ in range(4))[1:3]
+        ms = sum(ms) / 2
+        out[f"prefill_512_at_{p0}_ms"] = round(ms, 4)
+        out[f"prefill_512_at_{p0}_tflops"] = round(4.0 * B * 24 * 256 * (p0 + B / 2) / (ms * 1e-3) / 1e12, 1)
+    del kvr
+    return out
 
 
 def deltanet_extras(ops, torch, steps, L=48):

@@ -178,8 +178,8 @@ inline void attn_prefill(const float* q, const float* gate, const KVLayer& kv, K
     detail::check(qwa_attn_prefill(q, gate, &l, (int)kvt, B, p0, out16, st), "attn_prefill");
 }
 
-// set-up of the drop-in attn_prefill (no reference counterpart): the workspace of `st`, reserved where the engine
-// reserves attn_work_bytes (src/runtime/engine.cpp:724)
+// optional set-up of the drop-in attn_prefill (no reference counterpart): the workspace of `st`, reserved where the
+// engine reserves attn_work_bytes (src/runtime/engine.cpp:724); without it the first prefill on `st` reserves it
 inline void attn_prefill_reserve(int max_B, int max_pos, hipStream_t st) {
     detail::check(qwa_attn_prefill_reserve(max_B, max_pos, st), "attn_prefill_reserve");
 }

@@ -6,8 +6,9 @@
  * replaces.  Conventions:
  *   - all tensors are caller-owned device memory (out_host: host memory mapped for device access);
  *   - `stream` is a hipStream_t (NULL = the default stream); every call is asynchronous and stream-ordered;
- *   - no operator allocates memory; the decode `work` buffer is sized by qwa_attn_work_bytes(); the prefill workspace
- *     is reserved once per stream at set-up (qwa_attn_prefill_reserve) or passed in (qwa_attn_prefill_ws);
+ *   - the decode `work` buffer is sized by qwa_attn_work_bytes(); the prefill workspace is held per stream by the
+ *     library (reserved at set-up with qwa_attn_prefill_reserve, or on the stream's first prefill it does not
+ *     cover) or passed in (qwa_attn_prefill_ws); apart from that first-use growth no operator allocates memory;
  *   - the return value is a status code (QWA_OK = 0).  Invalid arguments are rejected before anything is launched
  *     (the reference aborts in the same situations, src/cuda/ops.cu:1002-1008); the C++ shim in q38rt_attn.hpp
  *     turns a nonzero status into abort() exactly like the reference.
@@ -120,16 +121,21 @@ int qwa_attn_prep_rows(const float* qg, const float* k, const float* v, const fl
 /* Replaces attn_prefill (src/cuda/prefill.cuh:59-60, src/cuda/prefill.cu:899-908): causal attention of B queries at
  * positions p0..p0+B-1 over the cache [0, p0+B), output * sigmoid(gate) as fp16 bits [B][6144].  fp16 MFMA, fp32
  * accumulation.  The reference's signature has no work buffer; this kernel needs one (fp16 tile images of the KV
- * range and split partial states), so the call uses the workspace reserved for its (device, stream) by
- * qwa_attn_prefill_reserve and returns QWA_ERR_RANGE when there is none or the call exceeds it.  It allocates
- * nothing, and calls on different streams use different workspaces. */
+ * range and split partial states), held by the library per (device, stream), so calls on different streams never
+ * share one.  A call the stream's workspace does not cover (the first call on a stream without a reservation, or a
+ * longer context) widens it first: hipMalloc of a workspace for max(p0 + B, twice the previous max_pos) positions
+ * (so a prompt prefilled chunk by chunk allocates O(log n) times); the buffer it replaces stays allocated until
+ * qwa_attn_prefill_release.  Under graph capture such a call returns QWA_ERR_RANGE instead (reserve before
+ * capturing).  Calls within the reservation allocate nothing. */
 int qwa_attn_prefill(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
                      uint16_t* out16, void* stream);
 
 /* Set-up for qwa_attn_prefill (no reference counterpart; the engine calls it where it reserves attn_work_bytes,
  * src/runtime/engine.cpp:724): allocates (hipMalloc) the workspace of `stream` on the current device for calls with
- * B <= max_B and p0 + B <= max_pos.  A second call for the same stream keeps a large-enough workspace or replaces a
- * smaller one (after synchronising the stream).  qwa_attn_prefill_release frees it (after synchronising). */
+ * B <= max_B and p0 + B <= max_pos.  A second call for the same stream keeps a large-enough workspace or allocates a
+ * larger one; the smaller one is not freed (a captured graph may still use it) until qwa_attn_prefill_release, which
+ * synchronises the stream and frees every workspace of the stream.  A graph that captured a prefill on the stream
+ * must not be replayed after its release.  Full context (262144 positions, B = 1024) costs ~1.2 GB per stream. */
 int qwa_attn_prefill_reserve(int max_B, int max_pos, void* stream);
 int qwa_attn_prefill_release(void* stream);
 

@@ -59,9 +59,12 @@ constexpr int NSLOT = 2 * NREC;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maximum (natural-log units)
 
+// the record slots of every valid call (up to MAXQ queries, any context up to MAX_POS): the size does not depend on
+// the context length
+constexpr size_t DEC_WORK_BYTES = (size_t)NSLOT * NKV * MAXQ * GRP * REC * sizeof(float);
 size_t dec_work_bytes(int n_pos) {
     (void)n_pos;
-    return (size_t)NSLOT * NKV * MAXQ * GRP * REC * sizeof(float);
+    return DEC_WORK_BYTES;
 }
 
 // One 16-key chunk in LDS.  K: piece-major, 16-byte piece p of row n at (16 p + n) * 16 (an MFMA operand read of one
@@ -1210,8 +1213,9 @@ namespace qwa {
 // every record a combine reads is written by the same call first.
 constexpr size_t DEC_SCRATCH_FLOATS = (size_t)NSLOT * NKV * MAXQ * GRP * REC;
 static __device__ __align__(256) float scratch[DEC_SCRATCH_FLOATS];
+// a change of the record layout must not outgrow the static array (dec_work_bytes covers every valid call)
+static_assert(DEC_SCRATCH_FLOATS * sizeof(float) >= DEC_WORK_BYTES, "decode scratch smaller than the work buffer");
 
-size_t dec_scratch_bytes() { return DEC_SCRATCH_FLOATS * sizeof(float); }
 
 static float* scratch_ptr(hipError_t* err) {
     constexpr int MAXDEV = 64;

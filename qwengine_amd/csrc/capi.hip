@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "launch.hpp"
+#include "pf_workspace.hpp"
 #include "qwattn_common.hpp"
 
 namespace {
@@ -51,24 +52,16 @@ int check_src(const qwa_row_src* s, int n, const char* what, const char* fn) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-// Prefill workspaces reserved at set-up, one per (device, stream): the drop-in attn_prefill keeps the reference's
-// signature (no work argument) and finds its stream's workspace here, so calls on different streams never share
-// scratch and no call allocates.
-struct PfReservation {
-    int dev;
-    void* stream;
-    void* ptr;
-    size_t bytes;
-    int max_B, max_pos;
-};
-std::mutex g_pf_mu;
-std::vector<PfReservation> g_pf;
-
-PfReservation* pf_find(int dev, void* stream) {
-    for (auto& r : g_pf)
-        if (r.dev == dev && r.stream == stream) return &r;
-    return nullptr;
-}
+// Prefill workspaces, one per (device, stream): the drop-in attn_prefill keeps the reference's signature (no work
+// argument) and finds its stream's workspace here, so calls on different streams never share scratch.  A stream gets
+// its workspace from qwa_attn_prefill_reserve at set-up, or on its first prefill that the reservation does not cover
+// (outside graph capture).  Buffers are freed only by qwa_attn_prefill_release (pf_workspace.hpp).
+int pf_alloc(void** p, size_t bytes) { return (int)hipMalloc(p, bytes); }
+int pf_free(void* p) { return (int)hipFree(p); }
+size_t pf_size(int B, int n_pos) { return qwa::prefill_work_bytes(B, n_pos); }
+using PfTable = qwa::PfWorkspaces<int (*)(void**, size_t), int (*)(void*), size_t (*)(int, int)>;
+std::mutex g_pf_mu;  // held from a workspace lookup until the call's kernels are enqueued
+PfTable g_pf(pf_alloc, pf_free, pf_size);
 
 // kernel timing window: each timed launch gets a slot of per-workgroup (start, end) stamps in a device buffer
 constexpr int PROF_MAX = 1024;     // launches per window
@@ -171,9 +164,7 @@ int qwa_attn_decode_multi_noalloc(const float* q, const float* gate, const qwa_k
     const char* fn = "attn_decode_multi_noalloc";
     int st;
     if ((st = check_decode(q, gate, kv, kvt, pos0, nq, out, oq, fn))) return st;
-    if (qwa::dec_work_bytes(pos0 + nq) > qwa::dec_scratch_bytes())
-        return fail(QWA_ERR_RANGE, "%s: the call needs %zu bytes of scratch, the library holds %zu", fn,
-                    qwa::dec_work_bytes(pos0 + nq), qwa::dec_scratch_bytes());
+    // the scratch array covers every call check_decode accepts (a static_assert next to it says so)
     return from_hip(qwa::launch_decode_noalloc(q, gate, *kv, kvt, pos0, nq, out, oq, out_host, as_stream(stream)), fn);
 }
 
@@ -260,51 +251,19 @@ int qwa_attn_prefill_reserve(int max_B, int max_pos, void* stream) {
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return from_hip(e, fn);
     std::lock_guard<std::mutex> lock(g_pf_mu);
-    PfReservation* r = pf_find(dev, stream);
-    // the workspace covers every call with B <= max_B and p0 + B <= max_pos (its size grows with both); a second
-    // reservation on the stream widens the first, so the size is that of both maxima together
-    if (r != nullptr) {
-        max_B = std::max(r->max_B, max_B);
-        max_pos = std::max(r->max_pos, max_pos);
-    }
-    const size_t need = qwa::prefill_work_bytes(max_B, max_pos);
-    if (r != nullptr && r->bytes >= need) {
-        r->max_B = max_B;
-        r->max_pos = max_pos;
-        return QWA_OK;
-    }
-    void* p = nullptr;
-    if ((e = hipMalloc(&p, need)) != hipSuccess) return from_hip(e, fn);
-    if (r != nullptr) {
-        // a smaller workspace of this stream: release it once the stream's queued work is done
-        if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess || (e = hipFree(r->ptr)) != hipSuccess) {
-            (void)hipFree(p);
-            return from_hip(e, fn);
-        }
-        r->ptr = p;
-        r->bytes = need;
-        r->max_B = max_B;
-        r->max_pos = max_pos;
-    } else {
-        g_pf.push_back(PfReservation{dev, stream, p, need, max_B, max_pos});
-    }
-    return QWA_OK;
+    // a second reservation on the stream widens the first; a workspace it replaces stays allocated until release
+    return from_hip((hipError_t)g_pf.reserve(dev, stream, max_B, max_pos), fn);
 }
 
 int qwa_attn_prefill_release(void* stream) {
+    const char* fn = "attn_prefill_release";
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return from_hip(e, "attn_prefill_release");
+    if (e != hipSuccess) return from_hip(e, fn);
     std::lock_guard<std::mutex> lock(g_pf_mu);
-    for (size_t i = 0; i < g_pf.size(); i++) {
-        if (g_pf[i].dev == dev && g_pf[i].stream == stream) {
-            if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess) return from_hip(e, "attn_prefill_release");
-            e = hipFree(g_pf[i].ptr);
-            g_pf.erase(g_pf.begin() + (long)i);
-            return from_hip(e, "attn_prefill_release");
-        }
-    }
-    return QWA_OK;
+    if (g_pf.find(dev, stream) == nullptr) return QWA_OK;
+    if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess) return from_hip(e, fn);
+    return from_hip((hipError_t)g_pf.release(dev, stream), fn);
 }
 
 int qwa_attn_prefill(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,
@@ -315,19 +274,23 @@ int qwa_attn_prefill(const float* q, const float* gate, const qwa_kv_layer* kv, 
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return from_hip(e, fn);
-    void* work = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(g_pf_mu);
-        const PfReservation* r = pf_find(dev, stream);
-        if (r == nullptr)
-            return fail(QWA_ERR_RANGE, "%s: no workspace reserved for this stream on device %d "
-                                       "(call qwa_attn_prefill_reserve at set-up)", fn, dev);
-        if (B > r->max_B || p0 + B > r->max_pos || qwa::prefill_work_bytes(B, p0 + B) > r->bytes)
-            return fail(QWA_ERR_RANGE, "%s: B = %d, p0 + B = %d beyond the stream's reservation (max_B %d, max_pos %d)",
-                        fn, B, p0 + B, r->max_B, r->max_pos);
-        work = r->ptr;
+    std::lock_guard<std::mutex> lock(g_pf_mu);  // until the kernels are enqueued (a release then waits for them)
+    qwa::PfSlot* r = g_pf.find(dev, stream);
+    if (!g_pf.covers(r, B, p0 + B)) {
+        // first use on this stream, or a call past its reservation: widen it, unless the stream is being captured
+        // (the graph would hold an allocation made inside the capture)
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if ((e = hipStreamIsCapturing(as_stream(stream), &cs)) != hipSuccess) return from_hip(e, fn);
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(QWA_ERR_RANGE, "%s: B = %d, p0 + B = %d during graph capture, beyond the stream's prefill "
+                                       "workspace (call qwa_attn_prefill_reserve before capturing)", fn, B, p0 + B);
+        // positions grow geometrically, so a prefill that walks a long prompt chunk by chunk allocates O(log n)
+        // times; the buffers it outgrows stay allocated until release
+        const int grow = r != nullptr ? std::min(qwa::MAX_POS, 2 * r->max_pos) : 0;
+        if ((e = (hipError_t)g_pf.reserve(dev, stream, B, std::max(p0 + B, grow))) != hipSuccess) return from_hip(e, fn);
+        r = g_pf.find(dev, stream);
     }
-    return from_hip(qwa::launch_prefill(q, gate, *kv, kvt, B, p0, out16, work, as_stream(stream)), fn);
+    return from_hip(qwa::launch_prefill(q, gate, *kv, kvt, B, p0, out16, r->ptr, as_stream(stream)), fn);
 }
 
 int qwa_attn_prefill_simple(const float* q, const float* gate, const qwa_kv_layer* kv, int kvt, int B, int p0,

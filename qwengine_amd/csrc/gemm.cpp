@@ -161,6 +161,10 @@ int qwa_gemm_tune(void* handle, const uint16_t* W, int N, int K, const uint16_t*
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
         return qwa_fail_status(QWA_ERR_INVALID, "gemm_tune: the stream is capturing (tune at set-up)");
+    // the candidates run with the handle's workspace, which belongs to its bound stream: work still queued there must
+    // finish first (a set-up call, so the wait is cheap)
+    if (st != g->stream && g->stream != nullptr && hipStreamSynchronize(g->stream) != hipSuccess)
+        return qwa_fail_status(QWA_ERR_HIP, "gemm_tune: synchronising the bound stream");
     constexpr int MAXC = 64;
     const int want = max_candidates < 1 ? 16 : (max_candidates > MAXC ? MAXC : max_candidates);
     GemmShape s;

@@ -45,7 +45,6 @@ size_t dec_work_bytes(int n_pos);
 hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int pos0, int nq,
                          void* work, float* out, const qwa_act_q8* oq, float* out_host, hipStream_t st);
 // the same decode on the library's static scratch (no allocation, no work argument)
-size_t dec_scratch_bytes();
 hipError_t launch_decode_noalloc(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int pos0, int nq,
                                  float* out, const qwa_act_q8* oq, float* out_host, hipStream_t st);
 hipError_t launch_decode_simple(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int n_pos,

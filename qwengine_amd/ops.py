@@ -340,8 +340,8 @@ def attn_prep_rows(qg, k, v, q_norm, k_norm, B: int, p0: int, rope, eps: float, 
 
 
 def attn_prefill(q, gate, kv: KVLayer, kvt, B: int, p0: int, out16, stream=None) -> None:
-    """src/cuda/prefill.cuh:59-60 (out16: fp16 [B, 6144]).  Uses the workspace reserved for the stream by
-    attn_prefill_reserve (raises QwaError without one); allocates nothing."""
+    """src/cuda/prefill.cuh:59-60 (out16: fp16 [B, 6144]).  Uses the stream's prefill workspace; a call it does not
+    cover widens it first (allocates), except under graph capture, where it raises QwaError."""
     _check(lib().qwa_attn_prefill(_ptr(q), _ptr(gate), ctypes.byref(kv.c()), _kvt(kvt), B, p0, _ptr(out16),
                                   _stream(stream)))
 

@@ -1,6 +1,6 @@
 // End-to-end drive of the attention path through the C++ shim (include/q38rt_attn.hpp), written the way the
 // reference engine calls its operators (src/runtime/engine.cpp:1587-1592 for decode, :2457-2479 for prefill):
-//   prefill of B tokens:  rope_table -> attn_prep_rows -> attn_prefill (drop-in call, reserved workspace)
+//   prefill of B tokens:  rope_table -> attn_prep_rows -> attn_prefill (drop-in call, workspace reserved on first use)
 //   decode of nq tokens:  attn_prep_multi (device RowSrc) -> attn_decode_multi (with the ActQ8 epilogue)
 // Test infrastructure: tests/test_gpu_shim_e2e.py writes the inputs, runs this program on the GPU and checks its
 // outputs against the ctypes path and the oracle.
@@ -97,7 +97,7 @@ int main(int argc, char** argv) {
     uint16_t* out16 = dev_alloc<uint16_t>((size_t)B * 6144);
     cuda::rope_table(0, B, theta, rope, st);
     cuda::attn_prep_rows(qg_pf, k_pf, v_pf, qn, kn, B, 0, rope, eps, kvt, kv, q_pf, gate_pf, st);
-    cuda::attn_prefill_reserve(B, B + nq, st);  // set-up, where the engine reserves its attention work
+    // no set-up call, as in the unchanged engine: the first prefill on the stream reserves its workspace
     cuda::attn_prefill(q_pf, gate_pf, kv, kvt, B, 0, reinterpret_cast<__half*>(out16), st);
 
     // ---- decode / verify of nq tokens at positions B..B+nq-1

@@ -5,7 +5,8 @@ against the FP32 test kernel at the reference's chunk cases (tests/kernels/test_
 tokens (the kernel cuts their key ranges into 6 and 7 splits; 500 and 512 take 5, the rest 8), long-context chunks
 of every format, the BASELINE 1024-token chunk at p0 = 32768 on all of its queries, and the ownership contract of
 the workspace: the caller-owned form gives the drop-in call's bits, a captured HIP graph replays correctly, two
-streams with their own workspaces do not interfere, and a stream without a reservation is refused."""
+streams with their own workspaces do not interfere, a stream without a reservation gets one on first use (outside
+graph capture), and a widened reservation keeps earlier captured graphs valid."""
 import numpy as np
 import pytest
 import torch
@@ -127,16 +128,76 @@ def test_prefill_caller_workspace_matches(gpu):
         ops.attn_prefill_ws(q, gate, kv, kvt, B, p0, out, work[:nbytes - 256])
 
 
-def test_prefill_without_reservation_is_refused(gpu):
+def test_prefill_without_reservation_reserves_on_first_use(gpu):
+    """The drop-in call needs no set-up call, as the reference's attn_prefill (src/cuda/prefill.cu:899-908): on a
+    stream with no reservation, and past a reservation that is too small, it widens the stream's workspace itself and
+    gives the caller-workspace bits."""
     kvt, p0, B = ops.Q8_0, 100, 16
     kv, q, gate = _inputs(kvt, p0, B, 80)
+    work = torch.empty(ops.attn_prefill_work_bytes(B, p0 + B), dtype=torch.uint8, device="cuda")
+    want = torch.empty((B, 24, 256), dtype=torch.float16, device="cuda")
+    ops.attn_prefill_ws(q, gate, kv, kvt, B, p0, want, work)
+    torch.cuda.synchronize()
+    for reserve_first in (False, True):
+        s = torch.cuda.Stream()
+        out = torch.full((B, 24, 256), float("nan"), dtype=torch.float16, device="cuda")
+        if reserve_first:
+            ops.attn_prefill_reserve(B, 50, stream=s)  # too small a window: the call widens it
+        torch.cuda.synchronize()
+        ops.attn_prefill(q, gate, kv, kvt, B, p0, out, stream=s)
+        s.synchronize()
+        assert torch.equal(out, want), reserve_first
+        ops.attn_prefill_release(stream=s)
+
+
+def test_prefill_capture_beyond_reservation_is_refused(gpu):
+    """Under graph capture a call the stream's workspace does not cover is refused (the graph would hold an
+    allocation made inside the capture); the capture itself stays usable for other work."""
+    kvt, p0, B = ops.Q8_0, 100, 16
+    kv, q, gate = _inputs(kvt, p0, B, 82)
     s = torch.cuda.Stream()
     out = torch.empty((B, 24, 256), dtype=torch.float16, device="cuda")
-    with pytest.raises(ops.QwaError, match="reserve"):
-        ops.attn_prefill(q, gate, kv, kvt, B, p0, out, stream=s)
-    ops.attn_prefill_reserve(B, 50, stream=s)  # too small a window
-    with pytest.raises(ops.QwaError, match="reservation"):
-        ops.attn_prefill(q, gate, kv, kvt, B, p0, out, stream=s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    err = None
+    with torch.cuda.graph(g, stream=s):
+        try:
+            ops.attn_prefill(q, gate, kv, kvt, B, p0, out, stream=s)
+        except ops.QwaError as e:
+            err = e
+        out.zero_()
+    assert err is not None and "capture" in str(err)
+    g.replay()
+    torch.cuda.synchronize()
+    del g
+    ops.attn_prefill_release(stream=s)
+
+
+def test_prefill_growth_keeps_captured_graph_valid(gpu):
+    """A graph captured with the stream's first workspace still replays correctly after a longer call has widened
+    the reservation (the replaced workspace stays allocated until release)."""
+    kvt, B = ops.Q8_0, 64
+    kv, q, gate = _inputs(kvt, 4000, B, 84)
+    want_short = _prefill(ops.attn_prefill, kv, q, gate, B, 200)
+    want_long = _prefill(ops.attn_prefill, kv, q, gate, B, 4000)
+    s = torch.cuda.Stream()
+    ops.attn_prefill_reserve(B, 200 + B, stream=s)
+    out = torch.full((B, 24, 256), float("nan"), dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        ops.attn_prefill(q, gate, kv, kvt, B, 200, out, stream=s)
+    out2 = torch.empty_like(out)
+    with torch.cuda.stream(s):
+        ops.attn_prefill(q, gate, kv, kvt, B, 4000, out2, stream=s)  # widens the reservation
+    s.synchronize()
+    assert np.array_equal(out2.float().cpu().numpy(), want_long)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.float().cpu().numpy(), want_short), f"replay {rep}"
+    del g
     ops.attn_prefill_release(stream=s)
 
 

@@ -36,6 +36,9 @@ def test_noalloc_decode_matches_work_buffer(gpu, kvt):
 
 
 def test_noalloc_decode_rejects_what_the_scratch_cannot_hold(gpu):
+    """The static scratch covers every call the decode accepts (a static_assert beside the array checks its size
+    against the record layout), so the calls it cannot hold are exactly those the decode's own rules reject: more
+    than 8 queries, contexts past 262144 positions."""
     kv, _, _ = make_cache(ops.Q4_0, 64, 64, seed=330)
     out = torch.empty((9, 24, 256), device="cuda")
     with pytest.raises(ops.QwaError, match="queries"):
