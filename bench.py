@@ -186,6 +186,7 @@ def main():
     calls = args.steps * L
     kern_us = kern_ms * 1000.0 / calls
     kern_dev_us = ops.profile_device_ms() * 1000.0 / calls
+    kern_mhz = ops.profile_clock_mhz()
     us_layer = ms_per_step * 1000.0 / L
     if args.copy_probe:
         src = torch.empty(1 << 27, dtype=torch.float32, device="cuda").fill_(1.0)
@@ -224,6 +225,7 @@ def main():
                      "kernel": "k_dec4 (split-K Q4_0 decode), kernel time per call averaged over the timed calls",
                      "kernel_us": round(kern_us, 3), "launches": kern_n, "calls": calls,
                      "kernel_us_device_clock": round(kern_dev_us, 3),
+                     "kernel_clock_mhz": round(kern_mhz, 1),
                      "algorithmic_bytes_per_launch": bytes_layer},
     }
 
@@ -320,12 +322,19 @@ def prefill_extras(ops, torch):
     pk_ms, pk_n = ops.profile_end()
     out["prefill_kernel_ms"] = round(pk_ms / max(pk_n, 1), 4)
     out["prefill_kernel_ms_device_clock"] = round(ops.profile_device_ms() / max(pk_n, 1), 4)
+    # the shader clock the kernel ran at, and its MFMA rate against the dense fp16 peak at that clock (256 CUs x 4
+    # SIMDs x 1024 fp16 flop per clock; 2.52 PFLOP/s at the 2.4 GHz that the published peak assumes)
+    mhz = ops.profile_clock_mhz()
+    out["prefill_kernel_clock_mhz"] = round(mhz, 1)
     flop = 4.0 * 24 * 256 * sum(p0 + t + 1 for t in range(B))
     tflops = flop / (ms * 1e-3) / 1e12
     out["prefill_1024_at_32768_ms"] = round(ms, 4)
     out["prefill_tflops"] = round(tflops, 1)
     out["prefill_mfma_frac"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
     out["prefill_kernel_mfma_frac"] = round(flop / (out["prefill_kernel_ms"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+    if mhz > 0:
+        out["prefill_kernel_mfma_frac_at_clock"] = round(
+            flop / (out["prefill_kernel_ms"] * 1e-3) / (256 * 4 * 1024 * mhz * 1e6), 4)
     del kv4
     # the reference's own prefill bench points (tests/kernels/test_attn_prefill.cu:79-101): B = 512 chunks at
     # p0 = 7680, 32256, 99488 over Q8_0, flop = 4 B 24 256 (p0 + B / 2) as it counts them

@@ -298,12 +298,15 @@ int qwa_gemm_tune(void* handle, const uint16_t* W, int N, int K, const uint16_t*
  * on its stream, and each of its workgroups records the device's realtime clock when it starts and ends.
  * qwa_profile_end() synchronizes the device and returns the summed event-to-event kernel time in ms and the number
  * of timed launches; qwa_profile_device_ms() then returns the same window's summed device-clock time (per launch:
- * last workgroup end - first workgroup start), which excludes the dispatch and completion latency the events include.
+ * last workgroup end - first workgroup start), which excludes the dispatch and completion latency the events include,
+ * and qwa_profile_clock_mhz() the shader clock the window's workgroups ran at (shader-clock ticks over realtime
+ * ticks, summed over every workgroup's lifetime), the clock against which MFMA busy cycles convert to time.
  * At most 1024 launches of at most 4096 workgroups per window; the first qwa_profile_begin() allocates the stamp
- * buffer (64 MiB), and events are created on first use; the library keeps both. */
+ * buffer (128 MiB), and events are created on first use; the library keeps both. */
 int qwa_profile_begin(void);
 int qwa_profile_end(double* total_ms, int* launches);
 int qwa_profile_device_ms(double* total_ms);
+int qwa_profile_clock_mhz(double* mhz);
 
 /* Human-readable text of a status code, and of the last error recorded by this library in the calling thread. */
 const char* qwa_status_string(int status);

@@ -34,6 +34,13 @@ namespace qwa {
 #ifdef QWA_TRACE
 // experimental phase stamps (trace builds only): [workgroup][8] realtime-clock values written by wave 0, lane 0
 static __device__ unsigned long long dec_trace[4096][8];
+// per-wave stamps: [workgroup][wave] first chunk landed, [workgroup][8 + wave] loop end
+static __device__ unsigned long long dec_wtrace[4096][16];
+#define WTRACE(k)                                                                                        \
+    do {                                                                                                 \
+        if ((threadIdx.x & 63) == 0)                                                                     \
+            dec_wtrace[blockIdx.x + gridDim.x * blockIdx.y][(k) + (threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
 #define TRACE(k)                                                                                         \
     do {                                                                                                 \
         if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][k] = __builtin_amdgcn_s_memrealtime(); \
@@ -41,6 +48,9 @@ static __device__ unsigned long long dec_trace[4096][8];
 #else
 #define TRACE(k) \
     do {         \
+    } while (0)
+#define WTRACE(k) \
+    do {          \
     } while (0)
 #endif
 
@@ -215,7 +225,10 @@ template <int WGW>
 __device__ __forceinline__ void pair_priority(int* s_prog, int wave, int lane, int j) {
     if (lane == 0) s_prog[wave] = j;
     const int other = s_prog[wave ^ (WGW / 2)];
-    if (j < other) __builtin_amdgcn_s_setprio(2);
+    // ties go to the younger wave (w >= WGW / 2), which the arbiter would otherwise hold back: with ties to the
+    // older one, the younger wave of a pair ended its loop ~1.5 us (one chunk) after it at 150000 positions
+    const bool behind = wave >= WGW / 2 ? j <= other : j < other;
+    if (behind) __builtin_amdgcn_s_setprio(2);
     else __builtin_amdgcn_s_setprio(0);
 }
 
@@ -859,6 +872,7 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
             if (NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
             else wait_vmcnt<0>();
             TRACE(2);
+            WTRACE(0);
             h4 P[1];
             VRegs vr;
             {
@@ -895,6 +909,7 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
             }
             pv(vr, P);
             TRACE(3);
+            WTRACE(8);
 #ifdef QWA_TRACE
             if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][5] = wsum;
             if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][6] = nmine;
@@ -1201,6 +1216,9 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
 }  // namespace qwa
 extern "C" int qwa_trace_read(unsigned long long* host, int nwg) {
     return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(qwa::dec_trace), sizeof(unsigned long long) * 8 * nwg);
+}
+extern "C" int qwa_wtrace_read(unsigned long long* host, int nwg) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(qwa::dec_wtrace), sizeof(unsigned long long) * 16 * nwg);
 }
 namespace qwa {
 #endif

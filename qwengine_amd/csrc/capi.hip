@@ -68,10 +68,11 @@ constexpr int PROF_MAX = 1024;     // launches per window
 struct Profile {
     bool on = false;
     int n = 0;
-    unsigned long long* stamps = nullptr;  // [PROF_MAX][PROF_MAX_WG][2], allocated on the first window
+    unsigned long long* stamps = nullptr;  // [PROF_MAX][PROF_MAX_WG][PROF_STAMPS], allocated on the first window
     std::vector<int> nwg;                  // workgroups of each timed launch
     std::vector<hipEvent_t> ev;            // 2 per launch (around it on its stream), created on first use
     double device_ms = 0.0;                // device-clock total of the last closed window
+    double clock_mhz = 0.0;                // shader clock over the workgroups' lifetimes in the last window
 } g_prof;
 
 }  // namespace
@@ -88,7 +89,7 @@ unsigned long long* profile_slot(int nwg, hipStream_t st) {
     }
     if (hipEventRecord(g_prof.ev[idx], st) != hipSuccess) return nullptr;
     g_prof.nwg.push_back(nwg);
-    return g_prof.stamps + (size_t)g_prof.n++ * PROF_MAX_WG * 2;
+    return g_prof.stamps + (size_t)g_prof.n++ * PROF_MAX_WG * PROF_STAMPS;
 }
 
 void profile_launched(unsigned long long* slot, hipStream_t st) {
@@ -482,7 +483,7 @@ int qwa_dequant_rows_f16(int fmt, const void* W, size_t row_bytes, int K, int ro
 }
 
 int qwa_profile_begin(void) {
-    const size_t bytes = (size_t)PROF_MAX * qwa::PROF_MAX_WG * 2 * sizeof(unsigned long long);
+    const size_t bytes = (size_t)PROF_MAX * qwa::PROF_MAX_WG * qwa::PROF_STAMPS * sizeof(unsigned long long);
     if (g_prof.stamps == nullptr) {
         const hipError_t e = hipMalloc(&g_prof.stamps, bytes);
         if (e != hipSuccess) {
@@ -499,28 +500,34 @@ int qwa_profile_begin(void) {
 }
 
 int qwa_profile_end(double* total_ms, int* launches) {
+    constexpr int NS = qwa::PROF_STAMPS;
     g_prof.on = false;
-    double tot = 0.0, dev_tot = 0.0;
+    double tot = 0.0, dev_tot = 0.0, clk_ticks = 0.0, rt_ticks = 0.0;
     const int n = g_prof.n;
     g_prof.device_ms = 0.0;
+    g_prof.clock_mhz = 0.0;
+    int khz = 0;
     if (n > 0) {
         hipError_t e = hipDeviceSynchronize();
         if (e != hipSuccess) return from_hip(e, "profile_end");
-        int dev = 0, khz = 0;
+        int dev = 0;
         e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
         if (e != hipSuccess) return from_hip(e, "profile_end");
         if (khz <= 0) return fail(QWA_ERR_HIP, "profile_end: no wall-clock rate");
-        std::vector<unsigned long long> h((size_t)n * qwa::PROF_MAX_WG * 2);
+        std::vector<unsigned long long> h((size_t)n * qwa::PROF_MAX_WG * NS);
         e = hipMemcpy(h.data(), g_prof.stamps, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost);
         if (e != hipSuccess) return from_hip(e, "profile_end");
         for (int i = 0; i < n; i++) {
-            const unsigned long long* st = h.data() + (size_t)i * qwa::PROF_MAX_WG * 2;
+            const unsigned long long* st = h.data() + (size_t)i * qwa::PROF_MAX_WG * NS;
             unsigned long long t0 = ~0ull, t1 = 0;
             for (int w = 0; w < g_prof.nwg[i]; w++) {
-                if (st[2 * w] == 0 || st[2 * w + 1] == 0) return fail(QWA_ERR_HIP, "profile_end: missing stamp");
-                t0 = st[2 * w] < t0 ? st[2 * w] : t0;
-                t1 = st[2 * w + 1] > t1 ? st[2 * w + 1] : t1;
+                const unsigned long long* s = st + (size_t)NS * w;
+                if (s[0] == 0 || s[1] == 0) return fail(QWA_ERR_HIP, "profile_end: missing stamp");
+                t0 = s[0] < t0 ? s[0] : t0;
+                t1 = s[1] > t1 ? s[1] : t1;
+                rt_ticks += (double)(s[1] - s[0]);
+                clk_ticks += (double)(s[3] - s[2]);
             }
             dev_tot += (double)(t1 - t0) / (double)khz;  // ticks / kHz = ms
             float ms = 0.0f;
@@ -530,6 +537,8 @@ int qwa_profile_end(double* total_ms, int* launches) {
         }
     }
     g_prof.device_ms = dev_tot;
+    // shader-clock ticks per realtime tick over every workgroup's lifetime, times the realtime rate
+    g_prof.clock_mhz = rt_ticks > 0.0 ? clk_ticks / rt_ticks * (double)khz / 1000.0 : 0.0;
     if (total_ms) *total_ms = tot;
     if (launches) *launches = n;
     g_prof.n = 0;
@@ -539,6 +548,11 @@ int qwa_profile_end(double* total_ms, int* launches) {
 
 int qwa_profile_device_ms(double* total_ms) {
     if (total_ms) *total_ms = g_prof.device_ms;
+    return QWA_OK;
+}
+
+int qwa_profile_clock_mhz(double* mhz) {
+    if (mhz) *mhz = g_prof.clock_mhz;
     return QWA_OK;
 }
 

@@ -8,10 +8,12 @@
 namespace qwa {
 
 // opt-in kernel timing (qwa_profile_begin / qwa_profile_end): before a main kernel launch of nwg workgroups the
-// launcher asks for a slot of 2 * nwg stamps (nullptr when timing is off; a HIP event is recorded on the stream), and
-// after the launch reports it (a second event); wave 0 of workgroup w writes the realtime clock at its start to
-// slot[2 w] and, after the workgroup's last store, at its end to slot[2 w + 1]
+// launcher asks for a slot of PROF_STAMPS * nwg stamps (nullptr when timing is off; a HIP event is recorded on the
+// stream), and after the launch reports it (a second event).  Wave 0 of workgroup w writes, at its start, the
+// realtime clock to slot[4 w] and the shader clock to slot[4 w + 2], and after the workgroup's last store the same
+// two clocks to slot[4 w + 1] and slot[4 w + 3]: their ratio is the shader clock the launch ran at.
 constexpr int PROF_MAX_WG = 4096;
+constexpr int PROF_STAMPS = 4;
 unsigned long long* profile_slot(int nwg, hipStream_t st);
 void profile_launched(unsigned long long* slot, hipStream_t st);
 
@@ -19,12 +21,18 @@ __device__ __forceinline__ int prof_wg() { return blockIdx.x + gridDim.x * (bloc
 // (wave 0 stores with all its lanes: a wave-uniform branch keeps the kernels' scalar operands uniform)
 __device__ __forceinline__ bool prof_wave0() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) == 0; }
 __device__ __forceinline__ void prof_start(unsigned long long* prof) {
-    if (prof != nullptr && prof_wave0()) prof[2 * prof_wg()] = __builtin_amdgcn_s_memrealtime();
+    if (prof != nullptr && prof_wave0()) {
+        prof[PROF_STAMPS * prof_wg()] = __builtin_amdgcn_s_memrealtime();
+        prof[PROF_STAMPS * prof_wg() + 2] = __builtin_amdgcn_s_memtime();
+    }
 }
 __device__ __forceinline__ void prof_end(unsigned long long* prof) {
     if (prof != nullptr) {
         __syncthreads();
-        if (prof_wave0()) prof[2 * prof_wg() + 1] = __builtin_amdgcn_s_memrealtime();
+        if (prof_wave0()) {
+            prof[PROF_STAMPS * prof_wg() + 1] = __builtin_amdgcn_s_memrealtime();
+            prof[PROF_STAMPS * prof_wg() + 3] = __builtin_amdgcn_s_memtime();
+        }
     }
 }
 

@@ -135,6 +135,7 @@ EXPORTS = {
     "qwa_profile_begin": (ctypes.c_int, []),
     "qwa_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
     "qwa_profile_device_ms": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double)]),
+    "qwa_profile_clock_mhz": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double)]),
     "qwa_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "qwa_last_error": (ctypes.c_char_p, []),
 }
@@ -390,6 +391,14 @@ def profile_device_ms() -> float:
     ms = ctypes.c_double(0.0)
     _check(lib().qwa_profile_device_ms(ctypes.byref(ms)))
     return ms.value
+
+
+def profile_clock_mhz() -> float:
+    """Shader clock (MHz) the last closed window's workgroups ran at: shader-clock ticks over realtime ticks, summed
+    over every workgroup's lifetime."""
+    mhz = ctypes.c_double(0.0)
+    _check(lib().qwa_profile_clock_mhz(ctypes.byref(mhz)))
+    return mhz.value
 
 
 def kv_packed_bytes(kvt, n_pos: int) -> int:
