@@ -99,6 +99,19 @@ def fill_cache(ops, torch, kvt, n, seed, outlier_frac=0.01):
     return kv
 
 
+SETTLE_S = 0.3  # seconds of untimed steps before a headline measurement
+
+
+def settle(torch, fn, seconds=SETTLE_S):
+    """Run fn untimed until `seconds` of wall time have passed (synchronising every few calls), so that the GPU's
+    clocks have left their transient after idle before anything is timed."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_calls(torch, fn, reps, warmup):
     for _ in range(warmup):
         fn()
@@ -164,7 +177,12 @@ def main():
         for kv in layers:
             ops.attn_decode_multi(q, gate, kv, kvt, n - nq, nq, work, out)
 
-    # ---- headline: W warmup steps, then exactly K timed steps
+    # ---- headline: the GPU's clock settling, W warmup steps, then exactly K timed steps.  After the caches are filled
+    # the per-step time of this workload rises from ~40 to ~53 us per layer within a few steps and settles at ~39 us
+    # only after ~25-30 steps (~18 ms of decode work, the GPU's power management adjusting its clocks; again after 2 s
+    # idle), so a few warmup steps would time the transient.  Untimed steps for SETTLE_S seconds come first, so that
+    # the K timed steps measure the steady state an engine decoding continuously runs at.
+    settle(torch, step)
     print(f"[bench] decode: {args.warmup} warmup + {args.steps} timed steps", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
         step()
@@ -311,8 +329,8 @@ def prefill_extras(ops, torch):
     gp = torch.randn((B, 24, 256), device="cuda")
     o16 = torch.empty((B, 24, 256), dtype=torch.float16, device="cuda")
     ops.attn_prefill_reserve(B, p0 + B)  # set-up: the stream's prefill workspace
-    # warm up, then the median of 4 groups of 5 calls
-    time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 1, 3)
+    # clocks settled (see the headline), then the median of 4 groups of 5 calls
+    settle(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16))
     ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 5, 0)
                 for _ in range(4))[1:3]
     ms = sum(ms) / 2
