@@ -32,6 +32,7 @@ METRIC = "decode attn µs/layer + HBM GB/s @150K Q4_0 KV; prefill attn TFLOP/s (
 TRAFFIC_PROFILE = os.path.join("profiles", "decode_q4_0_150k_hbm_traffic.md")
 DECODE_SOURCES = ("attn_decode.hip", "kv_operands.hpp", "launch.hpp", "qwattn_common.hpp")
 BYTES_PER_POS = {0: 4096, 1: 2176, 2: 1152}  # K + V values and scales over the 4 KV heads
+PROF_LAUNCHES = 1024  # launches one qwa_profile window times
 
 
 def parse():
@@ -196,12 +197,13 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
     # the dominant kernel alone: HIP events around each split-K decode launch (same stream), over the same work
+    # (the window holds PROF_LAUNCHES launches: at most that many calls are timed, one split-K launch per call)
+    prof_steps = max(1, min(args.steps, PROF_LAUNCHES // L))
     ops.profile_begin()
-    for _ in range(args.steps):
+    for _ in range(prof_steps):
         step()
     kern_ms, kern_n = ops.profile_end()
-    # per call (a 7-query verify is two launches: the split-K passes over row tiles 0-1 and tile 2)
-    calls = args.steps * L
+    calls = prof_steps * L
     kern_us = kern_ms * 1000.0 / calls
     kern_dev_us = ops.profile_device_ms() * 1000.0 / calls
     kern_mhz = ops.profile_clock_mhz()
