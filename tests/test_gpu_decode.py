@@ -270,3 +270,25 @@ def test_decode_at_max_positions(gpu, oracle, kvt, nq):
     assert_close(out.cpu().numpy(), ref, f"decode {KV_NAMES[kvt]} at {n} positions")
     with pytest.raises(ops.QwaError, match="262144"):
         _decode(kv, q, gate, n - nq + 1, nq)
+
+
+def test_profile_window_stamps(gpu):
+    """The opt-in timing window (qwa_profile_begin / end / device_ms / clock_mhz) over decode calls: one timed launch
+    per call, event time >= device-clock time > 0, a shader clock in the range the MI355X runs at, and the calls' bits
+    unchanged by the stamps."""
+    kvt, n = ops.Q4_0, 20000
+    kv, _, _ = make_cache(kvt, n + 1, n + 1, seed=91)
+    q, gate = _qg(1, 93)
+    want = _decode(kv, q, gate, n, 1)
+    work = torch.empty(ops.attn_work_bytes(n + 1) // 4 + 1, dtype=torch.float32, device="cuda")
+    out = torch.empty((1, 24, 256), device="cuda")
+    ops.profile_begin()
+    for _ in range(3):
+        ops.attn_decode_multi(q, gate, kv, kvt, n, 1, work, out)
+    ms, launches = ops.profile_end()
+    dev_ms, mhz = ops.profile_device_ms(), ops.profile_clock_mhz()
+    print(f"profile window: {launches} launches, {ms:.4f} ms events, {dev_ms:.4f} ms device, {mhz:.0f} MHz", flush=True)
+    assert launches == 3
+    assert ms >= dev_ms > 0.0
+    assert 500.0 < mhz < 3500.0
+    assert torch.equal(out, want)
