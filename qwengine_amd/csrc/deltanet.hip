@@ -317,59 +317,69 @@ size_t dn_work_bytes(int B) {
            sizeof(float);
 }
 
-// Per token t, channel c (grid (DN_CH / 256, B)): conv[t][c] = silu(sum_k w[c][k] in(t - 3 + k)), in(i) = qkv[i][c]
-// for i >= 0, else row 3 + i of the old window.  The q and k channels (blocks 0 .. 15, two heads of 128 each) are
-// not written out: the block L2-normalises its two heads through LDS (wave w < 2: head 2 x + w, lane holding dims
-// lane and lane + 64) into qn / kn.  Block 0 also writes beta and the decay of token t.  Only the v channels reach
-// r.conv.
+// Per channel c and run of DN_CR consecutive tokens (grid (DN_CH / 256, ceil(B / DN_CR))): conv[t][c] =
+// silu(sum_k w[c][k] in(t - 3 + k)), in(i) = qkv[i][c] for i >= 0, else row 3 + i of the old window.  A thread
+// slides the 4-tap window over its run, so each input row is read once per run instead of once per tap.  The q and
+// k channels (blocks x < 16, two heads of 128 each) are not written out: the block L2-normalises its heads through
+// LDS (wave w: the (token, head) pairs w, w + 4, ..., lane holding dims lane and lane + 64) into qn / kn.  Blocks
+// x = 0 also write beta and the decay of their tokens, and the run holding token B - 1 writes the window after the
+// chunk (rows k = input B - 3 + k) into the other buffer.  Only the v channels reach r.conv.
+constexpr int DN_CR = 8;  // tokens per thread of k_dn_conv_rows
 __global__ void __launch_bounds__(256) k_dn_conv_rows(const float* __restrict__ qkv, const float* __restrict__ cs_old,
                                                       const float* __restrict__ conv_w, DnRows r,
                                                       const float* __restrict__ beta_raw,
                                                       const float* __restrict__ alpha_raw,
                                                       const float* __restrict__ dt_bias,
-                                                      const float* __restrict__ ssm_a, float eps) {
-    __shared__ float sx[256];
-    const int t = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
+                                                      const float* __restrict__ ssm_a, float eps, int B,
+                                                      float* __restrict__ cs_new) {
+    __shared__ float sx[DN_CR][256];
+    const int t0 = blockIdx.y * DN_CR, c = blockIdx.x * 256 + threadIdx.x;
+    const int nt = min(DN_CR, B - t0);
     const float4 w = *reinterpret_cast<const float4*>(conv_w + (size_t)c * 4);
-    float x[4];
+    float x[DN_CR + 3];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int i = t - 3 + k;
-        x[k] = i >= 0 ? qkv[(size_t)i * DN_CH + c] : cs_old[(size_t)(3 + i) * DN_CH + c];
+    for (int k = 0; k < DN_CR + 3; k++) {
+        const int i = t0 - 3 + k;
+        x[k] = i < 0 ? cs_old[(size_t)(3 + i) * DN_CH + c] : i < B ? qkv[(size_t)i * DN_CH + c] : 0.0f;
     }
-    const float y = dn_silu(w.x * x[0] + w.y * x[1] + w.z * x[2] + w.w * x[3]);
+    if (t0 + DN_CR >= B) {
+        // the window after the chunk: inputs B - 3 .. B - 1 (x[B - t0 .. B - t0 + 2])
+#pragma unroll
+        for (int k = 0; k < DN_CR + 3; k++) {
+            const int i = t0 - 3 + k, kk = i - (B - 3);
+            if (kk >= 0 && kk < 3) cs_new[(size_t)kk * DN_CH + c] = x[k];
+        }
+    }
+    float y[DN_CR];
+#pragma unroll
+    for (int u = 0; u < DN_CR; u++) y[u] = dn_silu(w.x * x[u] + w.y * x[u + 1] + w.z * x[u + 2] + w.w * x[u + 3]);
     if (c >= 2 * DN_QK) {
-        r.conv[(size_t)t * DN_CH + c] = y;
+#pragma unroll
+        for (int u = 0; u < DN_CR; u++)
+            if (u < nt) r.conv[(size_t)(t0 + u) * DN_CH + c] = y[u];
         return;
     }
-    sx[threadIdx.x] = y;
+#pragma unroll
+    for (int u = 0; u < DN_CR; u++) sx[u][threadIdx.x] = y[u];
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave < 2) {
-        const int hc = 2 * blockIdx.x + wave;  // head of the q | k channels: q heads 0 .. 15, then k heads 0 .. 15
-        const float v0 = sx[128 * wave + lane], v1 = sx[128 * wave + lane + 64];
+    for (int pr = wave; pr < 2 * nt; pr += 4) {
+        const int u = pr >> 1, hw = pr & 1;
+        const int hc = 2 * blockIdx.x + hw;  // head of the q | k channels: q heads 0 .. 15, then k heads 0 .. 15
+        const float v0 = sx[u][128 * hw + lane], v1 = sx[u][128 * hw + lane + 64];
         const float iv = 1.0f / fmaxf(sqrtf(wave_sum(v0 * v0 + v1 * v1)), eps);
-        float* d = (hc < DN_KH ? r.qn + hc * DN_HD : r.kn + (hc - DN_KH) * DN_HD) + (size_t)t * DN_QK;
+        float* d = (hc < DN_KH ? r.qn + hc * DN_HD : r.kn + (hc - DN_KH) * DN_HD) + (size_t)(t0 + u) * DN_QK;
         d[lane] = v0 * iv;
         d[lane + 64] = v1 * iv;
-    } else if (blockIdx.x == 0 && (int)threadIdx.x - 128 < DN_VH) {
-        const int h = threadIdx.x - 128;
-        const float a = alpha_raw[(size_t)t * DN_VH + h] + dt_bias[h];
-        const float sp = a > 20.0f ? a : logf(1.0f + expf(a));
-        r.beta[(size_t)t * DN_VH + h] = 1.0f / (1.0f + expf(-beta_raw[(size_t)t * DN_VH + h]));
-        r.decay[(size_t)t * DN_VH + h] = expf(sp * ssm_a[h]);
     }
-}
-
-// the window after the B tokens (rows k = input B - 3 + k), into the other buffer
-__global__ void __launch_bounds__(256) k_dn_conv_state(const float* __restrict__ qkv, const float* __restrict__ cs_old,
-                                                       int B, float* __restrict__ cs_new) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= DN_CH) return;
-#pragma unroll
-    for (int k = 0; k < 3; k++) {
-        const int i = B - 3 + k;
-        cs_new[(size_t)k * DN_CH + c] = i >= 0 ? qkv[(size_t)i * DN_CH + c] : cs_old[(size_t)(3 + i) * DN_CH + c];
+    if (blockIdx.x == 0) {
+        for (int e = threadIdx.x; e < nt * DN_VH; e += 256) {
+            const int t = t0 + e / DN_VH, h = e % DN_VH;
+            const float a = alpha_raw[(size_t)t * DN_VH + h] + dt_bias[h];
+            const float sp = a > 20.0f ? a : logf(1.0f + expf(a));
+            r.beta[(size_t)t * DN_VH + h] = 1.0f / (1.0f + expf(-beta_raw[(size_t)t * DN_VH + h]));
+            r.decay[(size_t)t * DN_VH + h] = expf(sp * ssm_a[h]);
+        }
     }
 }
 
@@ -667,9 +677,8 @@ hipError_t launch_dn_rows(const qwa_dn_params& p, const float* qkv, const float*
     const DnRows r = dn_rows_split(work, B);
     const float* cs_old = p.conv_state + (size_t)cin * 3 * DN_CH;
     float* cs_new = p.conv_state + (size_t)(cin ^ 1) * 3 * DN_CH;
-    hipLaunchKernelGGL(k_dn_conv_rows, dim3(DN_CH / 256, B), dim3(256), 0, st, qkv, cs_old, p.conv_w, r, beta_raw,
-                       alpha_raw, p.dt_bias, p.ssm_a, eps);
-    hipLaunchKernelGGL(k_dn_conv_state, dim3(DN_CH / 256), dim3(256), 0, st, qkv, cs_old, B, cs_new);
+    hipLaunchKernelGGL(k_dn_conv_rows, dim3(DN_CH / 256, (B + DN_CR - 1) / DN_CR), dim3(256), 0, st, qkv, cs_old,
+                       p.conv_w, r, beta_raw, alpha_raw, p.dt_bias, p.ssm_a, eps, B, cs_new);
     const int nch = (B + DN_CT - 1) / DN_CT;
     hipLaunchKernelGGL(k_dn_chunk_prep, dim3(DN_VH, nch), dim3(256), 0, st, r, B);
     hipLaunchKernelGGL(k_dn_chunk_rows, dim3(DN_VH, DN_RG), dim3(DN_CW * 64), 0, st, r, p.ssm_state, B, core_out);
