@@ -425,9 +425,20 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
             f4 S[RT];
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) S[rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            uint32_t dcp[RT][4];  // per-tile copies of the scale dwords (as in the Q4_0 kernel's scores)
 #pragma unroll
             for (int b = 0; b < 8; b++) {
                 const h8 ka = k_block_int<KVT>(kst, i16, lg, b);
+                if (KVT != QWA_KV_F16 && (b & 1) == 0) {
+#pragma unroll
+                    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            dcp[rt][i] = kd[i][b >> 1];
+                            // measured: the copy gains with two tiles, not with three (one wave per SIMD)
+                            if (RT == 2 && rt == 0) asm("; tile scale copy" : "+v"(dcp[rt][i]));
+                        }
+                }
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
                     const h8 bh = QLDS ? s_q[((rt * 8 + b) * 2 + 0) * 64 + lane] : qh[QLDS ? 0 : rt][b];
@@ -441,7 +452,7 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
                         a = mfma16(ka, bl, a);
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
-                            const float d = h2f_bits((uint16_t)(kd[i][b >> 1] >> (16 * (b & 1))));
+                            const float d = h2f_bits((uint16_t)(dcp[rt][i] >> (16 * (b & 1))));
                             S[rt][i] = fmaf(d, a[i], S[rt][i]);
                         }
                     }
@@ -790,9 +801,22 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
         auto scores = [&](const KRegs& r, f4* S) {
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) S[rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            // each row tile scales its block products from its own copy of the scale dwords (an empty asm makes the
+            // copy): with one shared fp16 -> fp32 conversion the compiler issues a conversion plus an FMA per product
+            // for every tile after the first, instead of one mixed-precision FMA that reads the fp16 half directly
+            uint32_t dcp[RT][4];
 #pragma unroll
             for (int b = 0; b < 8; b++) {
                 const h8 ka = q4_codes(r.w[b], km);
+                if ((b & 1) == 0) {
+#pragma unroll
+                    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            dcp[rt][i] = r.d[i][b >> 1];
+                            if (rt + 1 < RT) asm("; tile scale copy" : "+v"(dcp[rt][i]));
+                        }
+                }
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
                     const h8 bh = QLDS ? s_q[((rt * 8 + b) * 2 + 0) * 64 + lane] : qh[QLDS ? 0 : rt][b];
@@ -801,7 +825,7 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
                     a = mfma16(ka, bl, a);
 #pragma unroll
                     for (int i = 0; i < 4; i++)
-                        S[rt][i] = fmaf(h2f_bits((uint16_t)(r.d[i][b >> 1] >> (16 * (b & 1)))), a[i], S[rt][i]);
+                        S[rt][i] = fmaf(h2f_bits((uint16_t)(dcp[rt][i] >> (16 * (b & 1)))), a[i], S[rt][i]);
                 }
             }
         };
