@@ -113,7 +113,10 @@ def settle(torch, fn, seconds=SETTLE_S):
         torch.cuda.synchronize()
 
 
-def time_calls(torch, fn, reps, warmup):
+def time_calls(torch, fn, reps, warmup, settle_s=SETTLE_S):
+    # every workload settles first, as the headline does: a new workload after another (or after idle) starts in the
+    # clock transient, which a few warmup calls do not cover
+    settle(torch, fn, settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -333,7 +336,7 @@ def prefill_extras(ops, torch):
     ops.attn_prefill_reserve(B, p0 + B)  # set-up: the stream's prefill workspace
     # clocks settled (see the headline), then the median of 4 groups of 5 calls
     settle(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16))
-    ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 5, 0)
+    ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp, gp, kv4, ops.Q8_0, B, p0, o16), 5, 0, settle_s=0.0)
                 for _ in range(4))[1:3]
     ms = sum(ms) / 2
     ops.profile_begin()
@@ -362,9 +365,9 @@ def prefill_extras(ops, torch):
     kvr = fill_cache(ops, torch, ops.Q8_0, 99488 + B, 4100, 0.0)
     ops.attn_prefill_reserve(B, 99488 + B)
     for p0 in (7680, 32256, 99488):
-        time_calls(torch, lambda: ops.attn_prefill(qp[:B], gp[:B], kvr, ops.Q8_0, B, p0, o16[:B]), 1, 2)
+        settle(torch, lambda: ops.attn_prefill(qp[:B], gp[:B], kvr, ops.Q8_0, B, p0, o16[:B]))
         ms = sorted(time_calls(torch, lambda: ops.attn_prefill(qp[:B], gp[:B], kvr, ops.Q8_0, B, p0, o16[:B]),
-                               5, 0) for _ in range(4))[1:3]
+                               5, 0, settle_s=0.0) for _ in range(4))[1:3]
         ms = sum(ms) / 2
         out[f"prefill_512_at_{p0}_ms"] = round(ms, 4)
         out[f"prefill_512_at_{p0}_tflops"] = round(4.0 * B * 24 * 256 * (p0 + B / 2) / (ms * 1e-3) / 1e12, 1)
