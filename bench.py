@@ -199,7 +199,8 @@ def main():
     e1.record()
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
-    # the dominant kernel alone: HIP events around each split-K decode launch (same stream), over the same work
+    # the dominant kernel alone: HIP events holding each split-K decode launch's own start / end timestamps (same
+    # stream, hipExtLaunchKernelGGL inside the library's timing window), over the same work
     # (the window holds PROF_LAUNCHES launches: at most that many calls are timed, one split-K launch per call)
     prof_steps = max(1, min(args.steps, PROF_LAUNCHES // L))
     ops.profile_begin()

@@ -294,8 +294,9 @@ int qwa_gemm_tune(void* handle, const uint16_t* W, int N, int K, const uint16_t*
 
 /* Opt-in kernel timing (no reference counterpart; the reference times phases with env-gated GPU timers,
  * src/runtime/engine.cpp:2477-2480): between qwa_profile_begin() and qwa_profile_end(), every launch of an
- * attention call's main kernel (decode: the split-K kernel; prefill: the MFMA kernel) is bracketed by two HIP events
- * on its stream, and each of its workgroups records the device's realtime clock when it starts and ends.
+ * attention call's main kernel (decode: the split-K kernel; prefill: the MFMA kernel) is launched with two HIP events
+ * that take the kernel's own start and end timestamps on its stream (hipExtLaunchKernelGGL; not while the stream is
+ * capturing), and each of its workgroups records the device's realtime clock when it starts and ends.
  * qwa_profile_end() synchronizes the device and returns the summed event-to-event kernel time in ms and the number
  * of timed launches; qwa_profile_device_ms() then returns the same window's summed device-clock time (per launch:
  * last workgroup end - first workgroup start), which excludes the dispatch and completion latency the events include,

@@ -1158,11 +1158,10 @@ constexpr bool PF3_VERIFY = QWA_DEC3 != 0;
 // passes of one or two tiles.  The kernel's 4-wave workgroups write half records into 2 nrec slots per KV head.
 template <int KVT>
 static bool dec3_pass(bool three, const float* q, const qwa_kv_layer& kv, int pos0, int nq, int t, int nrec,
-                      float* work, unsigned long long* prof, hipStream_t st) {
+                      float* work, const ProfSlot& ps, hipStream_t st) {
     if constexpr (KVT != QWA_KV_Q4_0) {
         if (three) {
-            hipLaunchKernelGGL((k_dec<KVT, 3, 4, 1>), dim3(2 * nrec, NKV), dim3(256), 0, st, q, kv, pos0, nq, t, work,
-                               prof);
+            QWA_LAUNCH_MAIN(ps, (k_dec<KVT, 3, 4, 1>), dim3(2 * nrec, NKV), dim3(256), st, q, kv, pos0, nq, t, work);
             return true;
         }
     }
@@ -1177,38 +1176,32 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
     // two row tiles share one pass over the cache; a third tile (6..8 queries) gets a pass of its own, in the same
     // launch, unless the one-pass three-tile kernel takes the call
     if (ONE_LAUNCH && rt == 3 && !three) {
-        unsigned long long* prof = profile_slot(2 * nrec * NKV, st);
+        const ProfSlot ps = profile_slot(2 * nrec * NKV, st);
         if constexpr (KVT == QWA_KV_Q4_0)
-            hipLaunchKernelGGL((k_dec4_3<Q4_WGW>), dim3(nrec, NKV, 2), dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, 0,
-                               work, prof);
+            QWA_LAUNCH_MAIN(ps, (k_dec4_3<Q4_WGW>), dim3(nrec, NKV, 2), dim3(64 * Q4_WGW), st, q, kv, pos0, nq, 0,
+                            work);
         else
-            hipLaunchKernelGGL((k_dec_3<KVT, DEC_WGW>), dim3(nrec, NKV, 2), dim3(64 * DEC_WGW), 0, st, q, kv, pos0, nq,
-                               0, work, prof);
-        profile_launched(prof, st);
+            QWA_LAUNCH_MAIN(ps, (k_dec_3<KVT, DEC_WGW>), dim3(nrec, NKV, 2), dim3(64 * DEC_WGW), st, q, kv, pos0, nq,
+                            0, work);
         return;
     }
     for (int t = 0; t < rt; t++) {
-        unsigned long long* prof = profile_slot((three ? 2 : 1) * nrec * NKV, st);  // three: 2 nrec half records
+        const ProfSlot ps = profile_slot((three ? 2 : 1) * nrec * NKV, st);  // three: 2 nrec half records
         if constexpr (KVT == QWA_KV_Q4_0) {
             if (t + 1 < rt) {
-                hipLaunchKernelGGL((k_dec4<2, 2, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work,
-                                   prof);
+                QWA_LAUNCH_MAIN(ps, (k_dec4<2, 2, Q4_WGW>), grid, dim3(64 * Q4_WGW), st, q, kv, pos0, nq, t, work);
                 t++;
             } else {
-                hipLaunchKernelGGL((k_dec4<2, 1, Q4_WGW>), grid, dim3(64 * Q4_WGW), 0, st, q, kv, pos0, nq, t, work,
-                                   prof);
+                QWA_LAUNCH_MAIN(ps, (k_dec4<2, 1, Q4_WGW>), grid, dim3(64 * Q4_WGW), st, q, kv, pos0, nq, t, work);
             }
-        } else if (dec3_pass<KVT>(three, q, kv, pos0, nq, t, nrec, work, prof, st)) {
+        } else if (dec3_pass<KVT>(three, q, kv, pos0, nq, t, nrec, work, ps, st)) {
             t += 2;
         } else if (t + 1 < rt) {
-            hipLaunchKernelGGL((k_dec<KVT, 2, DEC_WGW>), grid, dim3(64 * DEC_WGW), 0, st, q, kv, pos0, nq, t, work,
-                               prof);
+            QWA_LAUNCH_MAIN(ps, (k_dec<KVT, 2, DEC_WGW>), grid, dim3(64 * DEC_WGW), st, q, kv, pos0, nq, t, work);
             t++;
         } else {
-            hipLaunchKernelGGL((k_dec<KVT, 1, DEC_WGW>), grid, dim3(64 * DEC_WGW), 0, st, q, kv, pos0, nq, t, work,
-                               prof);
+            QWA_LAUNCH_MAIN(ps, (k_dec<KVT, 1, DEC_WGW>), grid, dim3(64 * DEC_WGW), st, q, kv, pos0, nq, t, work);
         }
-        profile_launched(prof, st);
     }
 }
 

@@ -692,16 +692,15 @@ static void launch_prefill_pass(const float* qp, const qwa_kv_layer& kv, int nb,
                                 hipStream_t st) {
     const int ns = pf_splits(nb);
     const dim3 grid((GRP * nb + PF_ROWS - 1) / PF_ROWS, NKV, ns);
-    unsigned long long* prof = profile_slot(grid.x * grid.y * grid.z, st);
-#define QWA_PF_LAUNCH(N)                                                                                            \
-    hipLaunchKernelGGL((k_prefill<KVT, PF_IMAGE, N>), grid, dim3(PF_THREADS), 0, st, qp, kv, nb, p0, w.img, w.tiles, \
-                       w.o, w.ml, w.ps, prof)
+    const ProfSlot ps = profile_slot(grid.x * grid.y * grid.z, st);
+#define QWA_PF_LAUNCH(N)                                                                                              \
+    QWA_LAUNCH_MAIN(ps, (k_prefill<KVT, PF_IMAGE, N>), grid, dim3(PF_THREADS), st, qp, kv, nb, p0, w.img, w.tiles, \
+                    w.o, w.ml, w.ps)
     if (ns == 5) QWA_PF_LAUNCH(5);
     else if (ns == 6) QWA_PF_LAUNCH(6);
     else if (ns == 7) QWA_PF_LAUNCH(7);
     else QWA_PF_LAUNCH(PF_NS);
 #undef QWA_PF_LAUNCH
-    profile_launched(prof, st);
 }
 
 hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer& kv, int kvt, int B, int p0,

@@ -79,21 +79,22 @@ struct Profile {
 
 namespace qwa {
 
-unsigned long long* profile_slot(int nwg, hipStream_t st) {
-    if (!g_prof.on || g_prof.stamps == nullptr || g_prof.n >= PROF_MAX || nwg > PROF_MAX_WG) return nullptr;
+ProfSlot profile_slot(int nwg, hipStream_t st) {
+    ProfSlot ps;
+    if (!g_prof.on || g_prof.stamps == nullptr || g_prof.n >= PROF_MAX || nwg > PROF_MAX_WG) return ps;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return ps;
     const size_t idx = 2 * (size_t)g_prof.n;
     while (g_prof.ev.size() <= idx + 1) {
         hipEvent_t e;
-        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return ps;
         g_prof.ev.push_back(e);
     }
-    if (hipEventRecord(g_prof.ev[idx], st) != hipSuccess) return nullptr;
     g_prof.nwg.push_back(nwg);
-    return g_prof.stamps + (size_t)g_prof.n++ * PROF_MAX_WG * PROF_STAMPS;
-}
-
-void profile_launched(unsigned long long* slot, hipStream_t st) {
-    if (slot != nullptr) (void)hipEventRecord(g_prof.ev[2 * (size_t)(g_prof.n - 1) + 1], st);
+    ps.start = g_prof.ev[idx];
+    ps.stop = g_prof.ev[idx + 1];
+    ps.stamps = g_prof.stamps + (size_t)g_prof.n++ * PROF_MAX_WG * PROF_STAMPS;
+    return ps;
 }
 
 }  // namespace qwa

@@ -1,6 +1,7 @@
 // Internal launchers (host side).  Argument validation lives in capi.hip; these assume valid arguments.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "qwattn.h"
@@ -8,14 +9,28 @@
 namespace qwa {
 
 // opt-in kernel timing (qwa_profile_begin / qwa_profile_end): before a main kernel launch of nwg workgroups the
-// launcher asks for a slot of PROF_STAMPS * nwg stamps (nullptr when timing is off; a HIP event is recorded on the
-// stream), and after the launch reports it (a second event).  Wave 0 of workgroup w writes, at its start, the
-// realtime clock to slot[4 w] and the shader clock to slot[4 w + 2], and after the workgroup's last store the same
-// two clocks to slot[4 w + 1] and slot[4 w + 3]: their ratio is the shader clock the launch ran at.
+// launcher asks for a slot of PROF_STAMPS * nwg stamps and a pair of HIP events (stamps == nullptr when timing is off
+// or the stream is capturing), and launches through QWA_LAUNCH_MAIN: under a window the launch goes through
+// hipExtLaunchKernelGGL, which gives the two events the kernel's own start and end timestamps on its stream.  Wave 0
+// of workgroup w writes, at its start, the realtime clock to slot[4 w] and the shader clock to slot[4 w + 2], and
+// after the workgroup's last store the same two clocks to slot[4 w + 1] and slot[4 w + 3]: their ratio is the shader
+// clock the launch ran at.
 constexpr int PROF_MAX_WG = 4096;
 constexpr int PROF_STAMPS = 4;
-unsigned long long* profile_slot(int nwg, hipStream_t st);
-void profile_launched(unsigned long long* slot, hipStream_t st);
+struct ProfSlot {
+    unsigned long long* stamps = nullptr;
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+ProfSlot profile_slot(int nwg, hipStream_t st);
+
+// launch of a main kernel whose last argument is the stamp slot
+#define QWA_LAUNCH_MAIN(PS, K, GRID, BLOCK, ST, ...)                                                           \
+    do {                                                                                                       \
+        if ((PS).stamps != nullptr)                                                                            \
+            hipExtLaunchKernelGGL(K, GRID, BLOCK, 0, ST, (PS).start, (PS).stop, 0u, __VA_ARGS__, (PS).stamps); \
+        else                                                                                                   \
+            hipLaunchKernelGGL(K, GRID, BLOCK, 0, ST, __VA_ARGS__, (unsigned long long*)nullptr);              \
+    } while (0)
 
 __device__ __forceinline__ int prof_wg() { return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); }
 // (wave 0 stores with all its lanes: a wave-uniform branch keeps the kernels' scalar operands uniform)
