@@ -303,7 +303,9 @@ int qwa_gemm_tune(void* handle, const uint16_t* W, int N, int K, const uint16_t*
  * and qwa_profile_clock_mhz() the shader clock the window's workgroups ran at (shader-clock ticks over realtime
  * ticks, summed over every workgroup's lifetime), the clock against which MFMA busy cycles convert to time.
  * At most 1024 launches of at most 4096 workgroups per window; the first qwa_profile_begin() allocates the stamp
- * buffer (128 MiB), and events are created on first use; the library keeps both. */
+ * buffer (128 MiB) on the current device, and events are created on first use; the library keeps both (a window
+ * opened on another device moves them there).  Launches on a device other than the window's go untimed.  The calls
+ * are serialised by a lock and may come from any host thread. */
 int qwa_profile_begin(void);
 int qwa_profile_end(double* total_ms, int* launches);
 int qwa_profile_device_ms(double* total_ms);

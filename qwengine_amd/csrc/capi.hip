@@ -73,7 +73,9 @@ struct Profile {
     std::vector<hipEvent_t> ev;            // 2 per launch (around it on its stream), created on first use
     double device_ms = 0.0;                // device-clock total of the last closed window
     double clock_mhz = 0.0;                // shader clock over the workgroups' lifetimes in the last window
+    int device = -1;                       // the device the stamp buffer lives on
 } g_prof;
+std::mutex g_prof_mu;  // the window's state is shared by every host thread that launches attention calls
 
 }  // namespace
 
@@ -81,7 +83,10 @@ namespace qwa {
 
 ProfSlot profile_slot(int nwg, hipStream_t st) {
     ProfSlot ps;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
     if (!g_prof.on || g_prof.stamps == nullptr || g_prof.n >= PROF_MAX || nwg > PROF_MAX_WG) return ps;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev != g_prof.device) return ps;  // launches on other devices go untimed
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return ps;
     const size_t idx = 2 * (size_t)g_prof.n;
@@ -485,12 +490,30 @@ int qwa_dequant_rows_f16(int fmt, const void* W, size_t row_bytes, int K, int ro
 
 int qwa_profile_begin(void) {
     const size_t bytes = (size_t)PROF_MAX * qwa::PROF_MAX_WG * qwa::PROF_STAMPS * sizeof(unsigned long long);
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    int dev = -1;
+    hipError_t de = hipGetDevice(&dev);
+    if (de != hipSuccess) return from_hip(de, "profile_begin");
+    if (g_prof.stamps != nullptr && dev != g_prof.device) {
+        // a window on another device: the stamp buffer and events follow it
+        int cur = dev;
+        de = hipSetDevice(g_prof.device);
+        if (de == hipSuccess) {
+            (void)hipFree(g_prof.stamps);
+            for (hipEvent_t ev : g_prof.ev) (void)hipEventDestroy(ev);
+            de = hipSetDevice(cur);
+        }
+        g_prof.stamps = nullptr;
+        g_prof.ev.clear();
+        if (de != hipSuccess) return from_hip(de, "profile_begin");
+    }
     if (g_prof.stamps == nullptr) {
         const hipError_t e = hipMalloc(&g_prof.stamps, bytes);
         if (e != hipSuccess) {
             g_prof.stamps = nullptr;
             return from_hip(e, "profile_begin");
         }
+        g_prof.device = dev;
     }
     const hipError_t e = hipMemset(g_prof.stamps, 0, bytes);
     if (e != hipSuccess) return from_hip(e, "profile_begin");
@@ -502,6 +525,7 @@ int qwa_profile_begin(void) {
 
 int qwa_profile_end(double* total_ms, int* launches) {
     constexpr int NS = qwa::PROF_STAMPS;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
     g_prof.on = false;
     double tot = 0.0, dev_tot = 0.0, clk_ticks = 0.0, rt_ticks = 0.0;
     const int n = g_prof.n;
@@ -548,11 +572,13 @@ int qwa_profile_end(double* total_ms, int* launches) {
 }
 
 int qwa_profile_device_ms(double* total_ms) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
     if (total_ms) *total_ms = g_prof.device_ms;
     return QWA_OK;
 }
 
 int qwa_profile_clock_mhz(double* mhz) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
     if (mhz) *mhz = g_prof.clock_mhz;
     return QWA_OK;
 }
