@@ -504,8 +504,11 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
             // the slot is consumed once these reads have returned: the refill's direct-to-LDS writes must not land
             // before them (a refill served from L2 returns within a few hundred cycles)
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            // refill the slot with the chunk NST ahead (clamped: re-reads cached lines at the end)
-            issue(ring[slot], chunk_key(j + NST));
+            // refill the slot with the class's next chunk, if it has one (with one slot every iteration waits for
+            // vmcnt 0, so a skipped refill needs no other wait; a clamped re-read of the last chunk would put one
+            // more memory round trip before the wave's merge)
+            static_assert(NST == 1, "the F16 / Q8_0 ring has one slot");
+            if (j + NST < nmine) issue(ring[slot], chunk_key(j + NST));
             constexpr int NW = sizeof(vr[0].w) / 4;  // raw words per 16 dims
             constexpr int DPW = 16 / NW;             // dims per raw word
 #pragma unroll
@@ -521,7 +524,7 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
                 }
             }
         }
-        wait_vmcnt<0>();  // drain the clamped prefetches before the ring is reused or the wave exits
+        wait_vmcnt<0>();  // nothing may still fly when the ring is reused or the wave exits
     }
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     TRACE(3);
