@@ -43,7 +43,7 @@ static __device__ unsigned long long dec_wtrace[4096][16];
     } while (0)
 #define TRACE(k)                                                                                         \
     do {                                                                                                 \
-        if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][k] = __builtin_amdgcn_s_memrealtime(); \
+        if (threadIdx.x == 0) dec_trace[prof_wg()][k] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #else
 #define TRACE(k) \
@@ -938,15 +938,17 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
             TRACE(3);
             WTRACE(8);
 #ifdef QWA_TRACE
-            if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][5] = wsum;
-            if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][6] = nmine;
-            if (threadIdx.x == 0) dec_trace[blockIdx.x + gridDim.x * blockIdx.y][7] = __builtin_amdgcn_s_memtime() - tloop;
+            if (threadIdx.x == 0) dec_trace[prof_wg()][5] = wsum;
+            if (threadIdx.x == 0) dec_trace[prof_wg()][6] = nmine;
+            if (threadIdx.x == 0) dec_trace[prof_wg()][7] = __builtin_amdgcn_s_memtime() - tloop;
 #endif
         } else {
+            TRACE(1);
             for (int j = 0; j < nmine; j++) {
                 pair_priority<WGW>(s_prog, wave, lane, DEC_INTERLEAVE ? j - nmine : j);
                 if (j + NST <= nmine) wait_vmcnt<Q4Chunk::NLOAD * (NST - 1)>();  // later chunks may still fly
                 else wait_vmcnt<0>();
+                if (j == 0) TRACE(2);
                 // two row tiles: V is read after the softmax, so K and V registers are never live together
                 f4 S[RT];
                 {
@@ -963,6 +965,7 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
                 if (j + NST < nmine) issue(j + NST);
                 pv(vr, P);
             }
+            TRACE(3);
         }
     }
 
