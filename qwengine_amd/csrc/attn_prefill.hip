@@ -77,10 +77,10 @@ constexpr float PF_LOG2E = 1.4426950408889634f;
 constexpr float PF_RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maximum (natural-log units)
 
 // Partial softmax states of one pass live in the caller's workspace: per split and output row
-// (row = token * NH + head, ps rows per split) O / l as 24-bit floats [split][row][HD] (pack24x4: fp32 rounded to
-// 15 mantissa bits, relative error <= 2^-16) and (m, l) as fp32 [split][row]; the combine reweights them by
-// l * exp(m - M).  (fp16 partials would halve the fp32 bytes but add a third fp16 rounding, up to 2^-12 |O|, on top
-// of the fp16 P and output of the reference's own MMA kernel: measured above the tolerance.)
+// (row = token * NH + head, ps rows per split) O / l as 16-bit fixed point [split][row][HD] against the row's largest
+// |O / l| (pack16x4; absolute error <= that maximum * 2^-16) and (m, l, scale) as fp32 [split][row]; the combine
+// reweights them by l * exp(m - M).  (fp16 partials would add a third fp16 rounding, up to 2^-12 |O|, on top of the
+// fp16 P and output of the reference's own MMA kernel: measured above the tolerance.)
 
 // raw bytes of one tile in LDS, in the cache's own layout: K rows, V rows, K scales, V scales (8 fp16 per row)
 template <int KVT> struct PfRaw {
@@ -332,17 +332,19 @@ __device__ __forceinline__ float rows_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Partial O / l values are stored as the top 24 bits of their fp32 pattern (sign, exponent, 15 mantissa bits),
-// rounded to nearest: 3 bytes per value, relative error <= 2^-16.  Four values pack into three dwords.
-__device__ __forceinline__ uint3 pack24x4(float a, float b, float c, float d) {
-    const uint32_t t0 = (__float_as_uint(a) + 0x80u) >> 8, t1 = (__float_as_uint(b) + 0x80u) >> 8;
-    const uint32_t t2 = (__float_as_uint(c) + 0x80u) >> 8, t3 = (__float_as_uint(d) + 0x80u) >> 8;
-    return make_uint3(t0 | (t1 << 24), (t1 >> 8) | (t2 << 16), (t2 >> 16) | (t3 << 8));
+// 16-bit partials: O / l of a (split, row) as signed 16-bit fixed point against the row's largest |O / l| (the scale
+// s = max / 32767 goes with (m, l)): absolute error <= s / 2 = max |O / l| * 2^-16 per value.
+__device__ __forceinline__ int pf_q16(float v) { return (int)fminf(fmaxf(__builtin_rintf(v), -32767.0f), 32767.0f); }
+__device__ __forceinline__ uint2 pack16x4(float a, float b, float c, float d) {
+    return make_uint2(((uint32_t)pf_q16(a) & 0xFFFFu) | ((uint32_t)pf_q16(b) << 16),
+                      ((uint32_t)pf_q16(c) & 0xFFFFu) | ((uint32_t)pf_q16(d) << 16));
 }
-__device__ __forceinline__ float4 unpack24x4(uint3 w) {
-    return make_float4(__uint_as_float(w.x << 8), __uint_as_float(((w.x >> 24) << 8) | ((w.y & 0xFFFFu) << 16)),
-                       __uint_as_float(((w.y >> 16) << 8) | ((w.z & 0xFFu) << 24)), __uint_as_float(w.z & 0xFFFFFF00u));
+__device__ __forceinline__ float4 unpack16x4(uint2 w) {
+    return make_float4((float)(int16_t)(w.x & 0xFFFFu), (float)(int16_t)(w.x >> 16), (float)(int16_t)(w.y & 0xFFFFu),
+                       (float)(int16_t)(w.y >> 16));
 }
+using PfPartO = uint2;    // four 16-bit values
+using PfPartMl = float4;  // (m, l, scale, unused)
 
 // One split of one row block: grid (row blocks, NKV, NS splits).  Tokens 0 .. B-1 of this pass sit at cache positions
 // p0 .. p0 + B - 1.
@@ -351,7 +353,7 @@ __device__ __forceinline__ float4 unpack24x4(uint3 w) {
 template <int KVT, bool IMG, int NS>
 __global__ void __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(PF_WPE, PF_WPE)))
 k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uint8_t* __restrict__ img, int img_tiles,
-          uint3* __restrict__ part_o, float2* __restrict__ part_ml, int ps, unsigned long long* prof) {
+          PfPartO* __restrict__ part_o, PfPartMl* __restrict__ part_ml, int ps, unsigned long long* prof) {
     prof_start(prof);
     using L = PfRaw<KVT>;
     constexpr int NBUF = IMG ? PF_IMG_NBUF : L::NBUF;
@@ -610,12 +612,20 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
         if (qpos[rt] < 0) continue;
         const int r = wrow0 + 16 * rt + i16, rr = (r / GRP) * NH + g * GRP + r % GRP;
         const size_t prow = (size_t)sp * ps + rr;
-        if (lg == 0) part_ml[prow] = make_float2(m[rt], lt);
         const float il = lt > 0.0f ? 1.0f / lt : 0.0f;  // a split that saw no key leaves l = 0 and O = 0
-        uint3* dst = part_o + prow * (HD / 4) + lg;
+        float amax = 0.0f;
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
-            dst[4 * dt] = pack24x4(o[rt][dt][0] * il, o[rt][dt][1] * il, o[rt][dt][2] * il, o[rt][dt][3] * il);
+#pragma unroll
+            for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(o[rt][dt][i]));
+        amax = rows_max(amax) * il;
+        const float qs = amax > 0.0f ? 32767.0f / amax : 0.0f;
+        const float f = il * qs;
+        if (lg == 0) part_ml[prow] = make_float4(m[rt], lt, amax * (1.0f / 32767.0f), 0.0f);
+        PfPartO* dst = part_o + prow * (HD / 4) + lg;
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++)
+            dst[4 * dt] = pack16x4(o[rt][dt][0] * f, o[rt][dt][1] * f, o[rt][dt][2] * f, o[rt][dt][3] * f);
     }
     prof_end(prof);
 }
@@ -625,18 +635,18 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
 // sum_s w_s (O_s / l_s) / sum_s w_s.
 template <int NS>
 __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ gate, int nrows,
-                                                    const uint3* __restrict__ part_o,
-                                                    const float2* __restrict__ part_ml, int ps,
+                                                    const PfPartO* __restrict__ part_o,
+                                                    const PfPartMl* __restrict__ part_ml, int ps,
                                                     uint16_t* __restrict__ out16) {
     const int rr = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (rr >= nrows) return;
-    float2 ml[NS];
+    PfPartMl ml[NS];
     float4 ov[NS];
     float mx = -INFINITY;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         ml[s] = part_ml[(size_t)s * ps + rr];
-        ov[s] = unpack24x4(part_o[((size_t)s * ps + rr) * (HD / 4) + lane]);
+        ov[s] = unpack16x4(part_o[((size_t)s * ps + rr) * (HD / 4) + lane]);
         mx = fmaxf(mx, ml[s].x);
     }
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -644,10 +654,11 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ ga
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         const float w = ml[s].x == -INFINITY ? 0.0f : fast_exp2((ml[s].x - mx) * PF_LOG2E) * ml[s].y;
-        acc.x += w * ov[s].x;
-        acc.y += w * ov[s].y;
-        acc.z += w * ov[s].z;
-        acc.w += w * ov[s].w;
+        const float wq = w * ml[s].z;  // the split's weight times its fixed-point scale
+        acc.x += wq * ov[s].x;
+        acc.y += wq * ov[s].y;
+        acc.z += wq * ov[s].z;
+        acc.w += wq * ov[s].w;
         wsum += w;
     }
     const float iw = 1.0f / wsum;
@@ -663,8 +674,8 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ ga
 // PF_MAXB)).
 struct PfWork {
     uint8_t* img;
-    float2* ml;
-    uint3* o;  // 24-bit values, 4 per uint3
+    PfPartMl* ml;
+    PfPartO* o;  // 4 values per element
     int tiles, ps;
     size_t bytes;
 };
@@ -676,11 +687,11 @@ static PfWork pf_work_layout(uint8_t* base, int B, int n_pos) {
     w.tiles = (n_pos - 1) / PF_TILE + 1;
     w.ps = NH * min(B, PF_MAXB);
     const size_t img = PF_IMAGE ? align256((size_t)NKV * w.tiles * PF_IMG_BYTES) : 0;
-    const size_t ml = align256((size_t)PF_NS * w.ps * sizeof(float2));
-    const size_t o = (size_t)PF_NS * w.ps * HD * 3;
+    const size_t ml = align256((size_t)PF_NS * w.ps * sizeof(PfPartMl));
+    const size_t o = (size_t)PF_NS * w.ps * (HD / 4) * sizeof(PfPartO);
     w.img = base;
-    w.ml = reinterpret_cast<float2*>(base + img);
-    w.o = reinterpret_cast<uint3*>(base + img + ml);
+    w.ml = reinterpret_cast<PfPartMl*>(base + img);
+    w.o = reinterpret_cast<PfPartO*>(base + img + ml);
     w.bytes = img + ml + o;
     return w;
 }
