@@ -619,9 +619,9 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
 #pragma unroll
             for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(o[rt][dt][i]));
         amax = rows_max(amax) * il;
-        const float qs = amax > 0.0f ? 32767.0f / amax : 0.0f;
+        const float qs = amax > 1e-30f ? 32767.0f / amax : 0.0f;  // (a row this small stores zeros: no inf scale)
         const float f = il * qs;
-        if (lg == 0) part_ml[prow] = make_float4(m[rt], lt, amax * (1.0f / 32767.0f), 0.0f);
+        if (lg == 0) part_ml[prow] = make_float4(m[rt], lt, qs > 0.0f ? amax * (1.0f / 32767.0f) : 0.0f, 0.0f);
         PfPartO* dst = part_o + prow * (HD / 4) + lg;
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
