@@ -42,6 +42,24 @@ def test_decode_vs_oracle(gpu, oracle, kvt, n_pos):
     assert err <= 5e-5, err
 
 
+@pytest.mark.parametrize("kvt", KVTS, ids=lambda k: KV_NAMES[k])
+@pytest.mark.parametrize("n_pos", [8192, 8193, 8208, 8209])
+def test_decode_class_chunk_counts(gpu, oracle, kvt, n_pos):
+    """8192 positions are 512 chunks, one per residue class; 8193 and 8209 give class 0 (8209: also class 1) a second,
+    one-key chunk, 8208 a full second chunk: a class's last chunk is not followed by a refill, whatever its count.
+    Against the oracle, and one query of a 7-query call against the same query decoded alone, bit for bit."""
+    print(f"decode class chunk counts kvt={KV_NAMES[kvt]} n_pos={n_pos}", flush=True)
+    kv, _, _ = make_cache(kvt, n_pos, 16384, seed=n_pos)
+    q, gate = _qg(7, 3 + n_pos)
+    out = _decode(kv, q[:1].contiguous(), gate[:1].contiguous(), n_pos - 1, 1)
+    Kd, Vd = dequant_cache(kv, n_pos)
+    ref = oracle.attention(q[:1].cpu().numpy(), gate[:1].cpu().numpy(), Kd, Vd, n_pos - 1, 1)
+    assert_close(out.cpu().numpy(), ref, f"decode {KV_NAMES[kvt]} n_pos={n_pos}")
+    multi = _decode(kv, q, gate, n_pos - 7, 7).cpu().numpy()
+    alone = _decode(kv, q[6:7].contiguous(), gate[6:7].contiguous(), n_pos - 1, 1).cpu().numpy()
+    assert np.array_equal(multi[6:7].view(np.uint32), alone.view(np.uint32))
+
+
 def test_config_c1_f16_4096(gpu, oracle):
     """single-token decode over an F16 cache of 4096 positions, on the tensors the CPU baseline
     times; against the float64 oracle and against the reference CPU arithmetic (oracle mode 1)."""
