@@ -563,14 +563,15 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
                 cr[rt] = mn == m[rt] ? 1.0f : fast_exp2((m[rt] - mn) * PF_LOG2E);  // m = -inf: c = 0
                 m[rt] = mn;
                 const float msl = mn == -INFINITY ? 0.0f : mn * PF_LOG2E;
-                float rs = 0.0f;
+                // the row's lane sum of the fp16 probabilities themselves (the weights P.V applies), two per dot2
                 h8 p;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float e = fast_exp2(fmaf(sc[rt][j >> 2][j & 3], PF_LOG2E, -msl));
-                    rs += e;
-                    p[j] = (_Float16)e;
-                }
+                for (int j = 0; j < 8; j++) p[j] = (_Float16)fast_exp2(fmaf(sc[rt][j >> 2][j & 3], PF_LOG2E, -msl));
+                const h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+                float rs = __builtin_amdgcn_fdot2(h2{p[0], p[1]}, one2, 0.0f, false);
+                rs = __builtin_amdgcn_fdot2(h2{p[2], p[3]}, one2, rs, false);
+                rs = __builtin_amdgcn_fdot2(h2{p[4], p[5]}, one2, rs, false);
+                rs = __builtin_amdgcn_fdot2(h2{p[6], p[7]}, one2, rs, false);
                 pb[rt] = p;
                 l[rt] = l[rt] * cr[rt] + rs;
             }
