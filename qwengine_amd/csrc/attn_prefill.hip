@@ -44,7 +44,6 @@ constexpr int PF_TILE = 32;                      // keys per tile
 constexpr int PF_KT = PF_TILE / 16;              // 16-key MFMA tiles per tile
 constexpr int PF_NS = PF_ROWS == 192 ? 6 : 8;    // key-range splits per row block (3 rounds of the chip for B = 1024)
 constexpr int PF_MAXB = 1024;                    // tokens per pass
-constexpr int PF_MAXROWS = PF_MAXB * NH;         // output rows per pass
 #ifndef QWA_PF_FILL
 #define QWA_PF_FILL 1
 #endif
