@@ -1155,8 +1155,10 @@ constexpr bool ONE_LAUNCH = QWA_ONE_LAUNCH != 0;
 // one launch; 7 queries, us per layer, one pass / two passes:
 //   F16  (from 32768 positions on):  24.4 / 20.3 at 4096, 46.4 / 45.0 at 16384, 85.9 / 107.1 at 65536,
 //                                    150 / 230 at 150000
-//   Q8_0 (from 131072 positions on): 23.1 / 19.4 at 4096, 43.5 / 34.7 at 16384, 81.5 / 74.6 at 65536,
-//                                    107.2 / 100.2 at 100000, 145.2 / 148.8-155.7 at 150000
+//   Q8_0 (from 212992 positions on): 23.1 / 19.4 at 4096, 43.5 / 34.7 at 16384, 81.5 / 74.6 at 65536,
+//                                    84.6 / 84.6 at 100000, 119.9 / 111.6 at 131072, 134.5 / 131.7 at 150000,
+//                                    168.4 / 167.2 at 200000, 209.0 / 219.8 at 262136
+//   (the Q8_0 figures from 100000 on: in-process A/B of the current kernels, whole call)
 // (Q8_0's int8 conversion hides behind the second wave of the two-tile pass.)  Q4_0 keeps two passes.
 constexpr bool PF3_VERIFY = QWA_DEC3 != 0;
 
@@ -1223,7 +1225,7 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     // 6..8 queries: the one-pass three-tile kernel where it is the faster path (every path gives the same bits)
     const int npos = pos0 + nq;
     const bool three = PF3_VERIFY && (GRP * nq + 15) / 16 == 3 &&
-                       ((kvt == QWA_KV_F16 && npos >= 32768) || (kvt == QWA_KV_Q8_0 && npos >= 131072));
+                       ((kvt == QWA_KV_F16 && npos >= 32768) || (kvt == QWA_KV_Q8_0 && npos >= 212992));
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, three, w, st);
     else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, three, w, st);
     else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, false, w, st);

@@ -247,12 +247,12 @@ def test_decode_in_hip_graph(gpu, kvt, n, nq):
 
 
 @pytest.mark.parametrize("kvt,nq,pos0", [(ops.F16, 7, 50000), (ops.F16, 4, 50000), (ops.Q8_0, 7, 50000),
-                                         (ops.Q8_0, 5, 50000), (ops.Q8_0, 7, 140000), (ops.Q4_0, 7, 50000)],
-                         ids=["f16-nq7", "f16-nq4", "q8_0-nq7", "q8_0-nq5", "q8_0-nq7-140k", "q4_0-nq7"])
+                                         (ops.Q8_0, 5, 50000), (ops.Q8_0, 7, 220000), (ops.Q4_0, 7, 50000)],
+                         ids=["f16-nq7", "f16-nq4", "q8_0-nq7", "q8_0-nq5", "q8_0-nq7-220k", "q4_0-nq7"])
 def test_verify_passes_long_context(gpu, oracle, kvt, nq, pos0):
     """The verify kernels at a context with several chunks per class: F16 with 6..8 queries in its one-pass
     three-tile kernel (half records folded by the combine), 4..5 queries in the two-tile pass, Q8_0 7 queries as two
-    passes in one launch at 50000 positions and in one pass at 140000, Q4_0 7 queries as two passes in one launch;
+    passes in one launch at 50000 positions and in one pass at 220000, Q4_0 7 queries as two passes in one launch;
     against the oracle, and each query bit-identical to its one-query decode."""
     print(f"verify long context kvt={KV_NAMES[kvt]} nq={nq}", flush=True)
     kv, _, _ = make_cache(kvt, pos0 + nq, pos0 + nq, seed=90 + nq)
