@@ -1148,13 +1148,17 @@ constexpr int DEC_WGW = WG_CLASSES;
 #endif
 // 6..8-query verify in two passes (two tiles, one tile): both as one launch
 constexpr bool ONE_LAUNCH = QWA_ONE_LAUNCH != 0;
+#ifndef QWA_F16_ONEPASS
+#define QWA_F16_ONEPASS 24576
+#endif
 #ifndef QWA_DEC3
 #define QWA_DEC3 1
 #endif
 // Three row tiles (6..8 queries) in one pass at one wave per SIMD, against the two passes (two tiles, one tile) as
 // one launch; 7 queries, us per layer, one pass / two passes:
-//   F16  (from 32768 positions on):  24.4 / 20.3 at 4096, 46.4 / 45.0 at 16384, 85.9 / 107.1 at 65536,
-//                                    150 / 230 at 150000
+//   F16  (from 24576 positions on):  24.4 / 20.3 at 4096, 36.1 / 31.5 at 8192, 43.6 / 41.9 at 16384,
+//                                    49.2 / 49.5 at 24576, 55.2 / 59.4 at 32775, 74.7 / 98.1 at 65536, 150 / 230 at
+//                                    150000 (8192 .. 65536: in-process A/B of the current kernels)
 //   Q8_0 (from 212992 positions on): 23.1 / 19.4 at 4096, 43.5 / 34.7 at 16384, 81.5 / 74.6 at 65536,
 //                                    84.6 / 84.6 at 100000, 119.9 / 111.6 at 131072, 134.5 / 131.7 at 150000,
 //                                    168.4 / 167.2 at 200000, 209.0 / 219.8 at 262136
@@ -1225,7 +1229,7 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     // 6..8 queries: the one-pass three-tile kernel where it is the faster path (every path gives the same bits)
     const int npos = pos0 + nq;
     const bool three = PF3_VERIFY && (GRP * nq + 15) / 16 == 3 &&
-                       ((kvt == QWA_KV_F16 && npos >= 32768) || (kvt == QWA_KV_Q8_0 && npos >= 212992));
+                       ((kvt == QWA_KV_F16 && npos >= QWA_F16_ONEPASS) || (kvt == QWA_KV_Q8_0 && npos >= 212992));
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, three, w, st);
     else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, three, w, st);
     else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, false, w, st);
