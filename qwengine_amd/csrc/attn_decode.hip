@@ -570,8 +570,8 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
     dec_body<KVT, RT, WGW, WPE>(s, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, prof);
 }
 
-// The two passes of a three-tile verify in one launch, grid (records, NKV, 2): z = 0 takes row tiles rt0 and rt0 + 1,
-// z = 1 tile rt0 + 2 (as k_dec4_3).
+// The two passes of a three-tile verify in one launch, grid (records, NKV): every workgroup runs the pass of row
+// tiles rt0 and rt0 + 1 over its classes, then the pass of tile rt0 + 2 (as k_dec4_3).
 template <int KVT, int WGW>
 __global__ void __launch_bounds__(64 * WGW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_dec_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
@@ -580,8 +580,11 @@ k_dec_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0,
         DecLds<KVT, 2, WGW, 2> two;
         DecLds<KVT, 1, WGW, 2> one;
     } s;
-    if (blockIdx.z == 0) dec_body<KVT, 2, WGW, 2>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, prof);
-    else dec_body<KVT, 1, WGW, 2>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, prof);
+    prof_start(prof);
+    dec_body<KVT, 2, WGW, 2>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, nullptr);
+    __syncthreads();  // the first pass's merge reads are done before the second pass's chunk loads land in LDS
+    dec_body<KVT, 1, WGW, 2>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, nullptr);
+    prof_end(prof);
 }
 
 // ---------------------------------------------------------------------------------------------- Q4_0 decode
@@ -1005,9 +1008,11 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
     dec4_body<NST, RT, WGW>(s, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, prof);
 }
 
-// The two passes of a three-tile verify in one launch, grid (records, NKV, 2): z = 0 takes row tiles rt0 and rt0 + 1,
-// z = 1 tile rt0 + 2.  The two-tile workgroups are dispatched first; the one-tile ones fill the CUs as they free up,
-// with no drain and ramp between two launches.  Each workgroup runs exactly the code of its own pass.
+// The two passes of a three-tile verify in one launch, grid (records, NKV): every workgroup runs the pass of row
+// tiles rt0 and rt0 + 1 over its classes and then the pass of tile rt0 + 2 over the same classes, each with exactly
+// the code of that pass (so a row's bits are those of any other kernel).  Against one workgroup per pass (a second
+// round of workgroups filling the CUs as the first frees them) this saves the second round's dispatch and set-up, and
+// the second pass re-reads chunks this CU has just brought through its L2.
 template <int WGW>
 __global__ void __launch_bounds__(WGW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_dec4_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
@@ -1016,8 +1021,11 @@ k_dec4_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0
         Dec4Lds<2, 2, WGW> two;
         Dec4Lds<2, 1, WGW> one;
     } s;
-    if (blockIdx.z == 0) dec4_body<2, 2, WGW>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, prof);
-    else dec4_body<2, 1, WGW>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, prof);
+    prof_start(prof);
+    dec4_body<2, 2, WGW>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, nullptr);
+    __syncthreads();  // the first pass's merge reads are done before the second pass's chunk loads land in LDS
+    dec4_body<2, 1, WGW>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, nullptr);
+    prof_end(prof);
 }
 
 
@@ -1188,13 +1196,11 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
     // two row tiles share one pass over the cache; a third tile (6..8 queries) gets a pass of its own, in the same
     // launch, unless the one-pass three-tile kernel takes the call
     if (ONE_LAUNCH && rt == 3 && !three) {
-        const ProfSlot ps = profile_slot(2 * nrec * NKV, st);
+        const ProfSlot ps = profile_slot(nrec * NKV, st);
         if constexpr (KVT == QWA_KV_Q4_0)
-            QWA_LAUNCH_MAIN(ps, (k_dec4_3<Q4_WGW>), dim3(nrec, NKV, 2), dim3(64 * Q4_WGW), st, q, kv, pos0, nq, 0,
-                            work);
+            QWA_LAUNCH_MAIN(ps, (k_dec4_3<Q4_WGW>), grid, dim3(64 * Q4_WGW), st, q, kv, pos0, nq, 0, work);
         else
-            QWA_LAUNCH_MAIN(ps, (k_dec_3<KVT, DEC_WGW>), dim3(nrec, NKV, 2), dim3(64 * DEC_WGW), st, q, kv, pos0, nq,
-                            0, work);
+            QWA_LAUNCH_MAIN(ps, (k_dec_3<KVT, DEC_WGW>), grid, dim3(64 * DEC_WGW), st, q, kv, pos0, nq, 0, work);
         return;
     }
     for (int t = 0; t < rt; t++) {
