@@ -30,7 +30,7 @@ METRIC = "decode attn µs/layer + HBM GB/s @150K Q4_0 KV; prefill attn TFLOP/s (
 # HBM bytes per k_dec4 launch at the headline workload come from the committed rocprofv3 PMC summary below.  It records
 # the digest of the decode kernel's sources it was measured on; a run on other sources reports traffic null.
 TRAFFIC_PROFILE = os.path.join("profiles", "decode_q4_0_150k_hbm_traffic.md")
-DECODE_SOURCES = ("attn_decode.hip", "kv_operands.hpp", "launch.hpp", "qwattn_common.hpp")
+DECODE_SOURCES = ("attn_decode.hip", "attn_decode_ilp.hip", "kv_operands.hpp", "launch.hpp", "qwattn_common.hpp")
 BYTES_PER_POS = {0: 4096, 1: 2176, 2: 1152}  # K + V values and scales over the 4 KV heads
 PROF_LAUNCHES = 1024  # launches one qwa_profile window times
 

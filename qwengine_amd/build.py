@@ -18,8 +18,8 @@ OUT_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(OUT_DIR, "libqwattn.so")
 ARCH = "gfx950"
 
-SOURCES = ["capi.hip", "kv_append.hip", "attn_decode.hip", "attn_simple.hip", "attn_prefill.hip", "deltanet.hip",
-           "gemv.hip", "gemm.cpp"]
+SOURCES = ["capi.hip", "kv_append.hip", "attn_decode.hip", "attn_decode_ilp.hip", "attn_simple.hip", "attn_prefill.hip",
+           "deltanet.hip", "gemv.hip", "gemm.cpp"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -46,7 +46,13 @@ def _hipcc() -> str:
 # per-source flags.  attn_decode.hip: MFMA results in VGPRs wherever the register budget allows.  Its one-wave-per-SIMD
 # verify kernels otherwise get their score MFMAs written to accumulation registers, and every block's product is then
 # copied out for its scale multiply (the Q8_0 three-tile kernel spilled 77 registers that way).
-FILE_FLAGS = {"attn_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# attn_decode_ilp.hip (the F16 one-pass three-tile verify kernel): the same, and LLVM's iterative-ILP machine
+# scheduler (latency hiding ahead of register economy).  deltanet.hip: that scheduler too (decode 6.1 -> 5.7 us,
+# 7-token verify 10.0 -> 9.5 us per layer; prefill unchanged).  The other sources measured the same or slower with it.
+ILP_SCHED = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
+FILE_FLAGS = {"attn_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+              "attn_decode_ilp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", *ILP_SCHED],
+              "deltanet.hip": ILP_SCHED}
 
 
 def _compile(src: str, extra: list[str], obj_dir: str) -> str:

@@ -72,10 +72,12 @@ constexpr float RESCALE_T = 8.0f;  // lazy-rescale threshold on the running maxi
 // the record slots of every valid call (up to MAXQ queries, any context up to MAX_POS): the size does not depend on
 // the context length
 constexpr size_t DEC_WORK_BYTES = (size_t)NSLOT * NKV * MAXQ * GRP * REC * sizeof(float);
+#ifndef QWA_DEC_KERNELS_ONLY
 size_t dec_work_bytes(int n_pos) {
     (void)n_pos;
     return DEC_WORK_BYTES;
 }
+#endif
 
 // One 16-key chunk in LDS.  K: piece-major, 16-byte piece p of row n at (16 p + n) * 16 (an MFMA operand read of one
 // quant block is then a conflict-free read at a fixed offset); V: row-major; then the K and V block scales
@@ -1029,6 +1031,16 @@ k_dec4_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0
 }
 
 
+#if !defined(QWA_DEC_KERNELS_ONLY) && !defined(QWA_TRACE)
+// Instantiated in attn_decode_ilp.hip, compiled with LLVM's iterative-ILP machine scheduler: the F16 one-pass
+// three-tile verify measured 1.5-1.8 us faster per layer that way (24576-150000 positions, 7 queries), while every
+// other kernel measured the same or slower (the Q4_0 two-tile pass +2 us at 150000 positions).  The schedule moves no
+// arithmetic, so the bits are those of any other build.  (Trace builds instantiate it here.)
+extern template __global__ void k_dec<QWA_KV_F16, 3, 4, 1>(const float* __restrict__, qwa_kv_layer, int, int, int,
+                                                           float* __restrict__, unsigned long long*);
+#endif
+
+#ifndef QWA_DEC_KERNELS_ONLY
 // Combine: one workgroup per (query t, head h, quarter of the head dims).  256 threads = 64 dims x 4 slices.
 // Sums run over fixed groups of CGRP consecutive splits, in split order inside a group and in group order across
 // groups: the summation tree depends only on split indices, never on nq (splits past a query's window hold l = 0
@@ -1296,5 +1308,6 @@ hipError_t launch_decode_noalloc(const float* q, const float* gate, const qwa_kv
     if (w == nullptr) return e;
     return launch_decode(q, gate, kv, kvt, pos0, nq, w, out, oq, out_host, st);
 }
+#endif  // QWA_DEC_KERNELS_ONLY
 
 }  // namespace qwa
