@@ -19,7 +19,7 @@ LIB = os.path.join(OUT_DIR, "libqwattn.so")
 ARCH = "gfx950"
 
 SOURCES = ["capi.hip", "kv_append.hip", "attn_decode.hip", "attn_decode_ilp.hip", "attn_simple.hip", "attn_prefill.hip",
-           "deltanet.hip", "gemv.hip", "gemm.cpp"]
+           "deltanet.hip", "gemv.hip", "gemv_mc.hip", "gemm.cpp"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -52,7 +52,9 @@ def _hipcc() -> str:
 ILP_SCHED = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
 FILE_FLAGS = {"attn_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
               "attn_decode_ilp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", *ILP_SCHED],
-              "deltanet.hip": ILP_SCHED}
+              "deltanet.hip": ILP_SCHED,
+              # gemv_mc.hip (IQ4_XS / IQ2_S one-column GEMV): the max-memory-clause scheduler
+              "gemv_mc.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
 
 
 def _compile(src: str, extra: list[str], obj_dir: str) -> str:

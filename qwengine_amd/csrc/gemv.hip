@@ -419,6 +419,21 @@ __global__ void __launch_bounds__(GV_WAVES * 64) k_gemv_q8(const uint8_t* __rest
     }
 }
 
+// The one-column instantiations of IQ4_XS and IQ2_S are compiled in gemv_mc.hip, with LLVM's max-memory-clause
+// machine scheduler (one-column GEMV at 6144 -> 5120: IQ4_XS 6.6 -> 6.15 us, IQ2_S 6.3 -> 6.1 us; the other formats
+// measured the same or slower with it).  The schedule moves no arithmetic.
+#define QWA_GV_KPARAMS                                                                                                \
+    const uint8_t* __restrict__, size_t, int, int, const int8_t* __restrict__, const float* __restrict__,            \
+        const float* __restrict__, int, float* __restrict__, int, int
+#define QWA_GV_ONE_COLUMN(PRE, FMT)                     \
+    PRE __global__ void k_gemv_q8<FMT, 1, 1>(QWA_GV_KPARAMS); \
+    PRE __global__ void k_gemv_q8<FMT, 1, 2>(QWA_GV_KPARAMS); \
+    PRE __global__ void k_gemv_q8<FMT, 1, 3>(QWA_GV_KPARAMS); \
+    PRE __global__ void k_gemv_q8<FMT, 1, 4>(QWA_GV_KPARAMS);
+#ifndef QWA_GV_KERNELS_ONLY
+QWA_GV_ONE_COLUMN(extern template, QWA_W_IQ4_XS)
+QWA_GV_ONE_COLUMN(extern template, QWA_W_IQ2_S)
+
 // ActQ8 of n_rows rows of K values (stride K): one 32-lane half-wave per 32-value block (src/cuda/gemv.cu:30-46)
 __global__ void __launch_bounds__(256) k_act_q8_rows(const float* __restrict__ x, int n_blocks, int8_t* __restrict__ q,
                                                      float* __restrict__ d, float* __restrict__ s) {
@@ -633,5 +648,7 @@ hipError_t launch_dequant_f16(int fmt, const void* W, size_t rb, int K, int rows
     }
     return hipGetLastError();
 }
+
+#endif  // QWA_GV_KERNELS_ONLY
 
 }  // namespace qwa
