@@ -43,7 +43,7 @@ static __device__ unsigned long long dec_wtrace[4096][16];
     } while (0)
 #define TRACE(k)                                                                                         \
     do {                                                                                                 \
-        if (threadIdx.x == 0) dec_trace[prof_wg()][k] = __builtin_amdgcn_s_memrealtime(); \
+        if (threadIdx.x == 0) dec_trace[prof_wg() + trace_base][k] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #else
 #define TRACE(k) \
@@ -56,6 +56,9 @@ static __device__ unsigned long long dec_wtrace[4096][16];
 
 constexpr int REC = 260;    // partial record: m, l, 2 pad, O[256] (16-byte aligned O)
 constexpr int CGRP = 16;    // combine: records per fixed summation group
+#ifndef QWA_Q4_CHAIN_FROM
+#define QWA_Q4_CHAIN_FROM 24576
+#endif
 #ifndef QWA_DEC_INTERLEAVE
 #define QWA_DEC_INTERLEAVE 1
 #endif
@@ -273,6 +276,55 @@ __device__ __forceinline__ void merge_split(MergeLdsN<WGW>& s, int wave, int lan
     for (int t = 0; t < TPW; t++) om[t] = oo[0][t];
 }
 
+// merge_split in two rounds of 8 dimension tiles, for workgroups whose LDS holds only half of MergeLdsN: round h
+// exchanges tiles 8 h .. 8 h + 7, which waves 4 h .. 4 h + 3 own (wave w still owns tiles 2 w and 2 w + 1).  Every
+// fold is merge_split's, on the same values in the same order, so the results are bit-identical.
+template <int WGW>
+struct MergeLdsH {
+    f4 o[WGW][8][64];
+    float ml[WGW][2][64];
+};
+
+template <int WGW>
+__device__ __forceinline__ void merge_split_half(MergeLdsH<WGW>& s, int wave, int lane, float& m, float& l,
+                                                 const f4* o, f4* om) {
+    static_assert(WGW == 8, "two rounds of 8 tiles: 4 owner waves of 2 tiles each per round");
+    constexpr int TPW = 16 / WGW;
+    l = half4_sum(l);
+    const float m_in = m, l_in = l;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        __syncthreads();  // every wave is done with the previous round's (or the previous merge's) reads
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) s.o[wave][dt][lane] = o[8 * h + dt];
+        if (h == 0) {
+            s.ml[wave][0][lane] = m_in;
+            s.ml[wave][1][lane] = l_in;
+        }
+        __syncthreads();
+        if ((wave >> 2) == h) {
+            float mm[WGW], ll[WGW];
+            f4 oo[WGW][TPW];
+#pragma unroll
+            for (int w = 0; w < WGW; w++) {
+                mm[w] = s.ml[w][0][lane];
+                ll[w] = s.ml[w][1][lane];
+#pragma unroll
+                for (int t = 0; t < TPW; t++) oo[w][t] = s.o[w][TPW * (wave - 4 * h) + t][lane];
+            }
+#pragma unroll
+            for (int step = 1; step < WGW; step *= 2)
+#pragma unroll
+                for (int w = 0; w < WGW; w += 2 * step)
+                    fold<TPW>(mm[w], ll[w], oo[w], mm[w + step], ll[w + step], oo[w + step]);
+            m = mm[0];
+            l = ll[0];
+#pragma unroll
+            for (int t = 0; t < TPW; t++) om[t] = oo[0][t];
+        }
+    }
+}
+
 // Q / 16 as fp16 hi + lo MFMA B-operand fragments of RT row tiles, written to LDS by the whole workgroup:
 // s_q[((rt * 8 + b) * 2 + part) * 64 + lane] holds, for lane (row i16, group lg) of tile rt0 + rt, the dims
 // 32 b + 8 lg + k_perm(j) (part 0: hi = fp16(Q / 16), part 1: lo = fp16(Q / 16 - hi)); padding rows are zero.
@@ -359,6 +411,10 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;  // chunks of this wave
     const size_t rowbase = (size_t)g * kv.capacity;
 
+#ifdef QWA_TRACE
+    // the one-tile pass of a three-tile verify stamps rows 2048 + workgroup (the two-tile pass rows 0 + workgroup)
+    const int trace_base = RT == 1 && rt0 >= 2 ? 2048 : 0;
+#endif
     TRACE(0);
     uint8_t(*ring)[C::BYTES] = s_u.a.ring[wave];
     auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * min(j, nmine - 1)); };
@@ -694,18 +750,57 @@ struct Dec4Lds {
         MergeLdsN<WGW> merge;
     } u;
     int prog[WGW];  // chunk index of each wave (pair_priority)
+    __device__ h8* qf() { return u.a.q; }
+    __device__ h8* qf_next() { return nullptr; }
+    __device__ uint8_t (*rings(int w))[Q4Chunk::BYTES] { return u.a.ring[w]; }
+    __device__ MergeLdsN<WGW>& mg() { return u.merge; }
+    __device__ MergeLdsH<WGW>& mg_half() { return *reinterpret_cast<MergeLdsH<WGW>*>(&u.merge); }
 };
 
-// One workgroup (record rec of KV head g) of the Q4_0 decode; its LDS is s.
-template <int NST, int RT, int WGW>
-__device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float* __restrict__ q, const qwa_kv_layer& kv,
-                                          int pos0, int nq, int rt0, float* __restrict__ work, int rec, int g,
+// LDS of the two chained passes of a three-tile verify (k_dec4_3<., true>): while the two-tile pass merges, the
+// rings (then holding the one-tile pass's first chunks) and the one-tile pass's Q fragments lie outside its merge
+// area, which therefore holds half of MergeLdsN (two merge rounds); the one-tile pass merges over the whole area.
+template <int WGW>
+struct Dec4ChainLds {
+    union {
+        struct {
+            uint8_t ring[WGW][2][Q4Chunk::BYTES];
+            h8 q1[8 * 2 * 64];  // the one-tile pass's fragments
+            union {
+                h8 q2[2 * 8 * 2 * 64];  // the two-tile pass's fragments
+                MergeLdsH<WGW> merge;   // the two-tile pass's merge (the rings are in use)
+            } u;
+        } a;
+        MergeLdsN<WGW> merge;  // the one-tile pass's merge (nothing else is in use any more)
+    } v;
+    int prog[WGW];
+};
+// the view of Dec4ChainLds that one of its passes works on (RT = 2: the first pass, RT = 1: the second)
+template <int RT, int WGW>
+struct Dec4ChainView {
+    Dec4ChainLds<WGW>& c;
+    int* prog;
+    __device__ explicit Dec4ChainView(Dec4ChainLds<WGW>& s) : c(s), prog(s.prog) {}
+    __device__ h8* qf() { return RT == 2 ? c.v.a.u.q2 : c.v.a.q1; }
+    __device__ h8* qf_next() { return RT == 2 ? c.v.a.q1 : nullptr; }
+    __device__ uint8_t (*rings(int w))[Q4Chunk::BYTES] { return c.v.a.ring[w]; }
+    __device__ MergeLdsH<WGW>& mg_half() { return c.v.a.u.merge; }
+    __device__ MergeLdsN<WGW>& mg() { return c.v.merge; }
+};
+
+// One workgroup (record rec of KV head g) of the Q4_0 decode; its LDS is s.  CHAIN = 1: the first of two chained
+// passes (it also stages the second pass's Q fragments, issues the second pass's first chunks once its own loop is
+// done, and merges in two rounds); CHAIN = 2: the second (its first chunks are in flight and its Q fragments in
+// LDS).  Both passes read the same chunks into the same ring slots, and the arithmetic of a row is that of CHAIN = 0.
+template <int NST, int RT, int WGW, int CHAIN = 0, class LDS = Dec4Lds<NST, RT, WGW>>
+__device__ __forceinline__ void dec4_body(LDS& s, const float* __restrict__ q, const qwa_kv_layer& kv, int pos0,
+                                          int nq, int rt0, float* __restrict__ work, int rec, int g,
                                           unsigned long long* prof) {
+    static_assert(CHAIN == 0 || NST == 2, "chained passes share one ring layout");
     prof_start(prof);
     constexpr bool QLDS = RT > 1;
-    auto& s_u = s.u;
     int* s_prog = s.prog;
-    h8* s_q = s_u.a.q;
+    h8* s_q = s.qf();
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
@@ -716,7 +811,7 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
     const int nmine = cls < nchunk ? (nchunk - 1 - cls) / DEC_CLASSES + 1 : 0;
     const size_t rowbase = (size_t)g * kv.capacity;
 
-    uint8_t(*ring)[Q4Chunk::BYTES] = s_u.a.ring[wave];
+    uint8_t(*ring)[Q4Chunk::BYTES] = s.rings(wave);
     const Q4Offsets off = q4_offsets(lane);
     auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * j); };
     auto issue = [&](int j) {
@@ -725,13 +820,18 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
         if (kb + CHUNK - 1 <= kmax) q4_issue_full(dst, kv, rowbase + kb, off, lane);
         else q4_issue_tail(dst, kv, rowbase, kb, kmax, lane);
     };
+#ifdef QWA_TRACE
+    // the one-tile pass of a three-tile verify stamps rows 2048 + workgroup (the two-tile pass rows 0 + workgroup)
+    const int trace_base = RT == 1 && rt0 >= 2 ? 2048 : 0;
+#endif
     TRACE(0);
     // the first chunk's loads go out before the Q set-up, so their latency overlaps it; the rest of the ring follows
     // the set-up, so the first iteration waits for chunk 0 only
-    if (nmine > 0) issue(0);
+    if (CHAIN != 2 && nmine > 0) issue(0);
 
     // Q / 16 as fp16 hi + lo fragments, loaded once per workgroup
-    q_frags_to_lds<QWA_KV_Q4_0, RT>(q, nq, g, rt0, s_q);
+    if constexpr (CHAIN != 2) q_frags_to_lds<QWA_KV_Q4_0, RT>(q, nq, g, rt0, s_q);
+    if constexpr (CHAIN == 1) q_frags_to_lds<QWA_KV_Q4_0, 1>(q, nq, g, rt0 + RT, s.qf_next());
     int qt[RT], hh[RT], qpos[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
@@ -762,9 +862,11 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
     }
 
     if (nmine > 0) {
+        if constexpr (CHAIN != 2) {
 #pragma unroll
-        for (int st = 1; st < NST; st++)
-            if (st < nmine) issue(st);
+            for (int st = 1; st < NST; st++)
+                if (st < nmine) issue(st);
+        }
         const Q4Masks km = q4_masks();
         const uint32_t bsel = (uint32_t)(i16 & 3) | 0x0c000c00u | ((uint32_t)(4 + (i16 & 3)) << 16);
         // K of chunk j from LDS: the 8 code dwords of this lane and the block scales of its 4 keys
@@ -972,6 +1074,12 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
             }
             TRACE(3);
         }
+        // the wave's ring is read out: the chained second pass's first chunks load while this pass merges
+        if constexpr (CHAIN == 1) {
+#pragma unroll
+            for (int st = 0; st < NST; st++)
+                if (st < nmine) issue(st);
+        }
     }
 
     __builtin_amdgcn_s_setprio(0);
@@ -981,7 +1089,8 @@ __device__ __forceinline__ void dec4_body(Dec4Lds<NST, RT, WGW>& s, const float*
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         f4 om[TPW];
-        merge_split<WGW>(s_u.merge, wave, lane, m[rt], l[rt], o[rt], om);
+        if constexpr (CHAIN == 1) merge_split_half<WGW>(s.mg_half(), wave, lane, m[rt], l[rt], o[rt], om);
+        else merge_split<WGW>(s.mg(), wave, lane, m[rt], l[rt], o[rt], om);
         const float lt = l[rt];  // already summed over the row's lanes by merge_split
         if (qpos[rt] >= 0) {
             float* recp = work + ((((size_t)rec * NKV + g) * MAXQ + qt[rt]) * GRP + hh[rt]) * REC;
@@ -1014,20 +1123,32 @@ k_dec4(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, 
 // tiles rt0 and rt0 + 1 over its classes and then the pass of tile rt0 + 2 over the same classes, each with exactly
 // the code of that pass (so a row's bits are those of any other kernel).  Against one workgroup per pass (a second
 // round of workgroups filling the CUs as the first frees them) this saves the second round's dispatch and set-up, and
-// the second pass re-reads chunks this CU has just brought through its L2.
-template <int WGW>
+// the second pass re-reads chunks this CU has just brought through its L2.  CHAIN: the passes are chained
+// (Dec4ChainLds), so the second pass's Q set-up and first chunks overlap the first pass's merge, at the price of that
+// merge running in two rounds.
+template <int WGW, bool CHAIN>
 __global__ void __launch_bounds__(WGW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_dec4_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
          unsigned long long* prof) {
-    __shared__ __attribute__((aligned(16))) union {
-        Dec4Lds<2, 2, WGW> two;
-        Dec4Lds<2, 1, WGW> one;
-    } s;
-    prof_start(prof);
-    dec4_body<2, 2, WGW>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, nullptr);
-    __syncthreads();  // the first pass's merge reads are done before the second pass's chunk loads land in LDS
-    dec4_body<2, 1, WGW>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, nullptr);
-    prof_end(prof);
+    if constexpr (CHAIN) {
+        __shared__ __attribute__((aligned(16))) Dec4ChainLds<WGW> s;
+        prof_start(prof);
+        Dec4ChainView<2, WGW> first(s);
+        dec4_body<2, 2, WGW, 1>(first, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, nullptr);
+        Dec4ChainView<1, WGW> second(s);
+        dec4_body<2, 1, WGW, 2>(second, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, nullptr);
+        prof_end(prof);
+    } else {
+        __shared__ __attribute__((aligned(16))) union {
+            Dec4Lds<2, 2, WGW> two;
+            Dec4Lds<2, 1, WGW> one;
+        } s;
+        prof_start(prof);
+        dec4_body<2, 2, WGW>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, nullptr);
+        __syncthreads();  // the first pass's merge reads are done before the second pass's chunk loads land in LDS
+        dec4_body<2, 1, WGW>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, nullptr);
+        prof_end(prof);
+    }
 }
 
 
@@ -1209,10 +1330,15 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
     // launch, unless the one-pass three-tile kernel takes the call
     if (ONE_LAUNCH && rt == 3 && !three) {
         const ProfSlot ps = profile_slot(nrec * NKV, st);
-        if constexpr (KVT == QWA_KV_Q4_0)
-            QWA_LAUNCH_MAIN(ps, (k_dec4_3<Q4_WGW>), grid, dim3(64 * Q4_WGW), st, q, kv, pos0, nq, 0, work);
-        else
+        // Q4_0: the chained passes from QWA_Q4_CHAIN_FROM positions on (bit-identical either way)
+        if constexpr (KVT == QWA_KV_Q4_0) {
+            if (pos0 + nq >= QWA_Q4_CHAIN_FROM)
+                QWA_LAUNCH_MAIN(ps, (k_dec4_3<Q4_WGW, true>), grid, dim3(64 * Q4_WGW), st, q, kv, pos0, nq, 0, work);
+            else
+                QWA_LAUNCH_MAIN(ps, (k_dec4_3<Q4_WGW, false>), grid, dim3(64 * Q4_WGW), st, q, kv, pos0, nq, 0, work);
+        } else {
             QWA_LAUNCH_MAIN(ps, (k_dec_3<KVT, DEC_WGW>), grid, dim3(64 * DEC_WGW), st, q, kv, pos0, nq, 0, work);
+        }
         return;
     }
     for (int t = 0; t < rt; t++) {
