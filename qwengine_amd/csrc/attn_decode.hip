@@ -59,6 +59,9 @@ constexpr int CGRP = 16;    // combine: records per fixed summation group
 #ifndef QWA_Q4_CHAIN_FROM
 #define QWA_Q4_CHAIN_FROM 24576
 #endif
+#ifndef QWA_Q8_CHAIN_FROM
+#define QWA_Q8_CHAIN_FROM 12288
+#endif
 #ifndef QWA_DEC_INTERLEAVE
 #define QWA_DEC_INTERLEAVE 1
 #endif
@@ -385,19 +388,59 @@ struct DecLds {
         } a;
         MergeLdsN<WGW> merge;
     } u;
+    __device__ h8* qf() { return u.a.q; }
+    __device__ h8* qf_next() { return nullptr; }
+    __device__ uint8_t (*rings(int w))[C::BYTES] { return u.a.ring[w]; }
+    __device__ int* progs() { return u.a.prog; }
+    __device__ MergeLdsN<WGW>& mg() { return u.merge; }
+    __device__ MergeLdsH<WGW>& mg_half() { return *reinterpret_cast<MergeLdsH<WGW>*>(&u.merge); }
 };
 
-// One workgroup (record rec of KV head g) of the F16 / Q8_0 decode; its LDS is s.
-template <int KVT, int RT, int WGW, int WPE>
-__device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const float* __restrict__ q,
-                                         const qwa_kv_layer& kv, int pos0, int nq, int rt0, float* __restrict__ work,
-                                         int rec, int g, unsigned long long* prof) {
+// LDS of the two chained passes of a Q8_0 three-tile verify (k_dec_3<Q8_0, ., true>), as Dec4ChainLds: the rings
+// and the one-tile pass's Q fragments lie outside the two-tile pass's merge area (two merge rounds), and the one-tile
+// pass merges over the whole area.  (F16 chunks are twice as large: its rings leave no room for it.)
+template <int KVT, int WGW>
+struct DecChainLds {
+    using C = ChunkLds<KVT>;
+    static_assert(DecCfg<KVT, 1>::NST == 1 && DecCfg<KVT, 2>::NST == 1, "one ring slot in both passes");
+    union {
+        struct {
+            uint8_t ring[WGW][1][C::BYTES];
+            h8 q1[8 * 2 * 64];  // the one-tile pass's fragments
+            union {
+                h8 q2[2 * 8 * 2 * 64];  // the two-tile pass's fragments
+                MergeLdsH<WGW> merge;   // the two-tile pass's merge (the rings are in use)
+            } u;
+        } a;
+        MergeLdsN<WGW> merge;  // the one-tile pass's merge
+    } v;
+    int prog[WGW];
+};
+template <int KVT, int RT, int WGW>
+struct DecChainView {
+    using C = ChunkLds<KVT>;
+    DecChainLds<KVT, WGW>& c;
+    __device__ explicit DecChainView(DecChainLds<KVT, WGW>& s) : c(s) {}
+    __device__ h8* qf() { return RT == 2 ? c.v.a.u.q2 : c.v.a.q1; }
+    __device__ h8* qf_next() { return RT == 2 ? c.v.a.q1 : nullptr; }
+    __device__ uint8_t (*rings(int w))[C::BYTES] { return c.v.a.ring[w]; }
+    __device__ int* progs() { return c.prog; }
+    __device__ MergeLdsN<WGW>& mg() { return c.v.merge; }
+    __device__ MergeLdsH<WGW>& mg_half() { return c.v.a.u.merge; }
+};
+
+// One workgroup (record rec of KV head g) of the F16 / Q8_0 decode; its LDS is s.  CHAIN as in dec4_body: 1 for the
+// first of two chained passes (it stages the second's Q fragments, issues the second's first chunk once its own loop
+// is done, and merges in two rounds), 2 for the second; the arithmetic of a row is that of CHAIN = 0.
+template <int KVT, int RT, int WGW, int WPE, int CHAIN = 0, class LDS = DecLds<KVT, RT, WGW, WPE>>
+__device__ __forceinline__ void dec_body(LDS& s, const float* __restrict__ q, const qwa_kv_layer& kv, int pos0,
+                                         int nq, int rt0, float* __restrict__ work, int rec, int g,
+                                         unsigned long long* prof) {
     prof_start(prof);
     using C = ChunkLds<KVT>;
     constexpr int NST = DecCfg<KVT, RT>::NST;
     constexpr bool QLDS = RT > 1;
-    constexpr bool PRIO = DecLds<KVT, RT, WGW, WPE>::PRIO;
-    auto& s_u = s.u;
+    constexpr bool PRIO = CHAIN != 0 || DecLds<KVT, RT, WGW, WPE>::PRIO;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
     const int kmax = pos0 + nq - 1;
@@ -416,20 +459,21 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
     const int trace_base = RT == 1 && rt0 >= 2 ? 2048 : 0;
 #endif
     TRACE(0);
-    uint8_t(*ring)[C::BYTES] = s_u.a.ring[wave];
+    uint8_t(*ring)[C::BYTES] = s.rings(wave);
     auto chunk_key = [&](int j) { return CHUNK * (cls + DEC_CLASSES * min(j, nmine - 1)); };
     const uint32_t koff = chunk_koff<KVT>(lane);
     auto issue = [&](uint8_t* dst, int kb) { issue_chunk<KVT>(dst, kv, rowbase, kb, kmax, lane, koff); };
     // the ring's loads go out before the Q set-up, so their HBM latency overlaps it
-    if (nmine > 0) {
+    if (CHAIN != 2 && nmine > 0) {
 #pragma unroll
         for (int st = 0; st < NST; st++) issue(ring[st], chunk_key(st));
     }
 
     // Q / 16 as fp16 hi + lo parts, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + perm(j);
     // the fragments are loaded once per workgroup through LDS
-    h8* s_q = s_u.a.q;
-    q_frags_to_lds<KVT, RT>(q, nq, g, rt0, s_q);
+    h8* s_q = s.qf();
+    if constexpr (CHAIN != 2) q_frags_to_lds<KVT, RT>(q, nq, g, rt0, s_q);
+    if constexpr (CHAIN == 1) q_frags_to_lds<KVT, 1>(q, nq, g, rt0 + RT, s.qf_next());
     __syncthreads();
     TRACE(1);
     h8 qh[QLDS ? 1 : RT][8], ql[QLDS ? 1 : RT][8];
@@ -460,7 +504,7 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
 
     if (nmine > 0) {
         for (int j = 0; j < nmine; j++) {
-            if constexpr (PRIO) pair_priority<WGW>(s_u.a.prog, wave, lane, DEC_INTERLEAVE ? j - nmine : j);
+            if constexpr (PRIO) pair_priority<WGW>(s.progs(), wave, lane, DEC_INTERLEAVE ? j - nmine : j);
             const int slot = j % NST;
             const int kb = chunk_key(j);
             wait_vmcnt<C::NLOAD * (NST - 1)>();  // this slot has landed; the later ones may still fly
@@ -583,6 +627,11 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
             }
         }
         wait_vmcnt<0>();  // nothing may still fly when the ring is reused or the wave exits
+        // the wave's ring is read out: the chained second pass's first chunk loads while this pass merges
+        if constexpr (CHAIN == 1) {
+#pragma unroll
+            for (int st = 0; st < NST; st++) issue(ring[st], chunk_key(st));
+        }
     }
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     TRACE(3);
@@ -594,7 +643,8 @@ __device__ __forceinline__ void dec_body(DecLds<KVT, RT, WGW, WPE>& s, const flo
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         f4 om[TPW];
-        merge_split<WGW>(s_u.merge, wave, lane, m[rt], l[rt], o[rt], om);
+        if constexpr (CHAIN == 1) merge_split_half<WGW>(s.mg_half(), wave, lane, m[rt], l[rt], o[rt], om);
+        else merge_split<WGW>(s.mg(), wave, lane, m[rt], l[rt], o[rt], om);
         const int r = 16 * (rt0 + rt) + i16;
         const int qt = r / GRP, hh = r % GRP;
         const float lt = l[rt];  // already summed over the row's lanes by merge_split
@@ -629,20 +679,32 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
 }
 
 // The two passes of a three-tile verify in one launch, grid (records, NKV): every workgroup runs the pass of row
-// tiles rt0 and rt0 + 1 over its classes, then the pass of tile rt0 + 2 (as k_dec4_3).
-template <int KVT, int WGW>
+// tiles rt0 and rt0 + 1 over its classes, then the pass of tile rt0 + 2 (as k_dec4_3; CHAIN: chained as there, Q8_0
+// only).
+template <int KVT, int WGW, bool CHAIN>
 __global__ void __launch_bounds__(64 * WGW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_dec_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
         unsigned long long* prof) {
-    __shared__ __attribute__((aligned(16))) union {
-        DecLds<KVT, 2, WGW, 2> two;
-        DecLds<KVT, 1, WGW, 2> one;
-    } s;
-    prof_start(prof);
-    dec_body<KVT, 2, WGW, 2>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, nullptr);
-    __syncthreads();  // the first pass's merge reads are done before the second pass's chunk loads land in LDS
-    dec_body<KVT, 1, WGW, 2>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, nullptr);
-    prof_end(prof);
+    if constexpr (CHAIN) {
+        static_assert(KVT == QWA_KV_Q8_0, "chained passes: Q8_0 (F16 rings are too large)");
+        __shared__ __attribute__((aligned(16))) DecChainLds<KVT, WGW> s;
+        prof_start(prof);
+        DecChainView<KVT, 2, WGW> first(s);
+        dec_body<KVT, 2, WGW, 2, 1>(first, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, nullptr);
+        DecChainView<KVT, 1, WGW> second(s);
+        dec_body<KVT, 1, WGW, 2, 2>(second, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, nullptr);
+        prof_end(prof);
+    } else {
+        __shared__ __attribute__((aligned(16))) union {
+            DecLds<KVT, 2, WGW, 2> two;
+            DecLds<KVT, 1, WGW, 2> one;
+        } s;
+        prof_start(prof);
+        dec_body<KVT, 2, WGW, 2>(s.two, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, nullptr);
+        __syncthreads();  // the first pass's merge reads are done before the second pass's chunk loads land in LDS
+        dec_body<KVT, 1, WGW, 2>(s.one, q, kv, pos0, nq, rt0 + 2, work, blockIdx.x, blockIdx.y, nullptr);
+        prof_end(prof);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------- Q4_0 decode
@@ -1336,8 +1398,12 @@ static void launch_dec_kvt(const float* q, const qwa_kv_layer& kv, int pos0, int
                 QWA_LAUNCH_MAIN(ps, (k_dec4_3<Q4_WGW, true>), grid, dim3(64 * Q4_WGW), st, q, kv, pos0, nq, 0, work);
             else
                 QWA_LAUNCH_MAIN(ps, (k_dec4_3<Q4_WGW, false>), grid, dim3(64 * Q4_WGW), st, q, kv, pos0, nq, 0, work);
+        } else if (KVT == QWA_KV_Q8_0 && pos0 + nq >= QWA_Q8_CHAIN_FROM) {
+            // Q8_0: the chained passes from QWA_Q8_CHAIN_FROM positions on (bit-identical either way)
+            QWA_LAUNCH_MAIN(ps, (k_dec_3<KVT, DEC_WGW, KVT == QWA_KV_Q8_0>), grid, dim3(64 * DEC_WGW), st, q, kv, pos0,
+                            nq, 0, work);
         } else {
-            QWA_LAUNCH_MAIN(ps, (k_dec_3<KVT, DEC_WGW>), grid, dim3(64 * DEC_WGW), st, q, kv, pos0, nq, 0, work);
+            QWA_LAUNCH_MAIN(ps, (k_dec_3<KVT, DEC_WGW, false>), grid, dim3(64 * DEC_WGW), st, q, kv, pos0, nq, 0, work);
         }
         return;
     }

@@ -84,22 +84,25 @@ def test_decode_multi_vs_oracle(gpu, oracle, kvt, nq):
     assert_close(out.cpu().numpy(), ref, f"verify {KV_NAMES[kvt]} nq={nq}")
 
 
+@pytest.mark.parametrize("kvt", [ops.Q4_0, ops.Q8_0], ids=lambda k: KV_NAMES[k])
 @pytest.mark.parametrize("nq", [6, 7, 8])
-def test_q4_verify_chained_passes_bit_identical(gpu, oracle, nq):
-    """Q4_0 verify with 6..8 queries runs its two passes chained from 24576 covered positions on (the one-tile
-    pass's first chunks load while the two-tile pass merges, in two rounds) and unchained below.  Calls that end on
-    either side of that boundary give every query the bits of the same query decoded alone, and the oracle's values."""
-    print(f"q4 verify chained passes nq={nq}", flush=True)
-    n_pos = 24584
-    kv, _, _ = make_cache(ops.Q4_0, n_pos, 32768, seed=40 + nq)
+def test_verify_chained_passes_bit_identical(gpu, oracle, kvt, nq):
+    """Q4_0 / Q8_0 verify with 6..8 queries runs its two passes chained from 24576 / 12288 covered positions on (the
+    one-tile pass's first chunks load while the two-tile pass merges, in two rounds) and unchained below.  Calls that
+    end on either side of that boundary give every query the bits of the same query decoded alone, and the oracle's
+    values."""
+    print(f"verify chained passes kvt={KV_NAMES[kvt]} nq={nq}", flush=True)
+    bound = 24576 if kvt == ops.Q4_0 else 12288
+    n_pos = bound + 8
+    kv, _, _ = make_cache(kvt, n_pos, 32768, seed=40 + nq)
     q, gate = _qg(8, 91 + nq)
     q, gate = q[:nq].contiguous(), gate[:nq].contiguous()
     Kd, Vd = dequant_cache(kv, n_pos)
-    for end in (24575, 24576, 24584):  # positions the call covers: pos0 + nq
+    for end in (bound - 1, bound, bound + 8):  # positions the call covers: pos0 + nq
         pos0 = end - nq
         out = _decode(kv, q, gate, pos0, nq).cpu().numpy()
         ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, pos0, nq)
-        assert_close(out, ref, f"q4 verify nq={nq} end={end}")
+        assert_close(out, ref, f"verify {KV_NAMES[kvt]} nq={nq} end={end}")
         for t in range(nq):
             alone = _decode(kv, q[t:t + 1].contiguous(), gate[t:t + 1].contiguous(), pos0 + t, 1).cpu().numpy()
             assert np.array_equal(out[t].view(np.uint32), alone[0].view(np.uint32)), (end, t)
