@@ -1351,6 +1351,9 @@ constexpr int DEC_WGW = WG_CLASSES;
 #endif
 // 6..8-query verify in two passes (two tiles, one tile): both as one launch
 constexpr bool ONE_LAUNCH = QWA_ONE_LAUNCH != 0;
+#ifndef QWA_Q8_ONEPASS
+#define QWA_Q8_ONEPASS 212992
+#endif
 #ifndef QWA_F16_ONEPASS
 #define QWA_F16_ONEPASS 24576
 #endif
@@ -1439,7 +1442,7 @@ hipError_t launch_decode(const float* q, const float* gate, const qwa_kv_layer& 
     // 6..8 queries: the one-pass three-tile kernel where it is the faster path (every path gives the same bits)
     const int npos = pos0 + nq;
     const bool three = PF3_VERIFY && (GRP * nq + 15) / 16 == 3 &&
-                       ((kvt == QWA_KV_F16 && npos >= QWA_F16_ONEPASS) || (kvt == QWA_KV_Q8_0 && npos >= 212992));
+                       ((kvt == QWA_KV_F16 && npos >= QWA_F16_ONEPASS) || (kvt == QWA_KV_Q8_0 && npos >= QWA_Q8_ONEPASS));
     if (kvt == QWA_KV_F16) launch_dec_kvt<QWA_KV_F16>(q, kv, pos0, nq, nsplit, three, w, st);
     else if (kvt == QWA_KV_Q8_0) launch_dec_kvt<QWA_KV_Q8_0>(q, kv, pos0, nq, nsplit, three, w, st);
     else launch_dec_kvt<QWA_KV_Q4_0>(q, kv, pos0, nq, nsplit, false, w, st);
