@@ -58,6 +58,25 @@ inline int pf_splits(int nb) {
         if ((long)((groups * ns + 255) / 256) * best < (long)((groups * best + 255) / 256) * ns) best = ns;
     return best;
 }
+#ifndef QWA_PF_UPW
+#define QWA_PF_UPW 1
+#endif
+#ifndef QWA_PF_SEG_MAXPOS
+#define QWA_PF_SEG_MAXPOS 81920
+#endif
+// (row block, KV head, split) units per workgroup of a pass of nb tokens whose keys end at npos: as many as make the
+// units one round of the chip's 256 CUs, when the split count is 8 (so the workgroups of one XCD walk the splits in
+// step, see k_prefill) and the pass's keys end within QWA_PF_SEG_MAXPOS; otherwise 1, the units running in rounds.
+// Measured, whole call, 1024 tokens (in-process A/B against rounds): Q8_0 -31 us at p0 = 0, -30 at 8192, -43 at
+// 32768, -43 at 49152, -23 at 65536, +19 at 100000 (Q4_0 -48 at 32768, -12 at 100000; F16 -41 at 32768).  Past
+// ~80000 positions a workgroup's three splits are long enough for the row blocks sharing an XCD's L2 to drift apart.
+// (QWA_PF_UPW = 0: always rounds.)
+inline int pf_units_per_wg(int nb, int npos) {
+    const int ns = pf_splits(nb);
+    if (!QWA_PF_UPW || ns != 8 || npos > QWA_PF_SEG_MAXPOS) return 1;
+    const int units = (GRP * nb + PF_ROWS - 1) / PF_ROWS * NKV * ns;
+    return (units + 255) / 256;
+}
 constexpr int KS_LD = HD + 8;                    // K tile row stride (halves)
 constexpr int VT_LD = PF_TILE + 8;               // V^T tile row stride (halves)
 #ifndef QWA_PF_VD
@@ -352,7 +371,7 @@ using PfPartMl = float4;  // (m, l, scale, unused)
 template <int KVT, bool IMG, int NS>
 __global__ void __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(PF_WPE, PF_WPE)))
 k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uint8_t* __restrict__ img, int img_tiles,
-          PfPartO* __restrict__ part_o, PfPartMl* __restrict__ part_ml, int ps, unsigned long long* prof) {
+          PfPartO* __restrict__ part_o, PfPartMl* __restrict__ part_ml, int ps, int upw, unsigned long long* prof) {
     prof_start(prof);
     using L = PfRaw<KVT>;
     constexpr int NBUF = IMG ? PF_IMG_NBUF : L::NBUF;
@@ -362,29 +381,57 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
     __shared__ __attribute__((aligned(16))) _Float16 s_vt[IMG ? 1 : 2][IMG ? 8 : HD * VT_LD];
     const int t = threadIdx.x, lane = t & 63, i16 = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane((int)(t >> 6));
+    // Work units: (KV head g, row block bx, split) triples.  upw = 1: one unit per workgroup, grid (row blocks, NKV,
+    // NS).  upw > 1: grid (units / upw), workgroup w takes units upw w .. upw w + upw - 1 of the list ordered by
+    // (g, bx, split); a run of consecutive splits of one (g, bx) is one key range, walked as one segment (one online
+    // softmax) that leaves one partial state, in the slot of its first split (k_pf_combine merges only those).  The
+    // workgroups that one XCD runs (w = x mod 8) then all start at split (upw x) mod NS and move through the splits in
+    // step, so they read the same image tiles at the same time, as the XCD-aware numbering of upw = 1 arranges.
+    const int nrb = (GRP * B + PF_ROWS - 1) / PF_ROWS;
+    const int units = nrb * NKV * NS;
+    int unit = upw == 1 ? 0 : (int)blockIdx.x * upw;
+    const int unit_end = upw == 1 ? 1 : min(unit + upw, units);
+    for (int seg = 0; unit < unit_end; seg++) {
+    int bx, g, sp, sp_last;
+    if (upw == 1) {
 #if QWA_PF_XCD
-    // XCD-aware numbering: workgroup lin is dispatched to XCD lin % 8; give each XCD whole (KV head, split) pairs, so
-    // the row blocks that read the same image tiles share one L2
-    // (a split count with NKV x NS not a multiple of 8 keeps the plain numbering)
-    int bx = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
-    if constexpr ((NKV * NS) % 8 == 0) {
-        const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-        const int xcd = lin & 7, slot = lin >> 3, nrb = gridDim.x;
-        const int pair = NKV * NS / 8 * xcd + slot / nrb;
-        bx = slot % nrb;
-        g = pair % NKV;
-        sp = pair / NKV;
-    }
+        // XCD-aware numbering: workgroup lin is dispatched to XCD lin % 8; give each XCD whole (KV head, split) pairs,
+        // so the row blocks that read the same image tiles share one L2
+        // (a split count with NKV x NS not a multiple of 8 keeps the plain numbering)
+        bx = blockIdx.x;
+        g = blockIdx.y;
+        sp = blockIdx.z;
+        if constexpr ((NKV * NS) % 8 == 0) {
+            const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+            const int xcd = lin & 7, slot = lin >> 3;
+            const int pair = NKV * NS / 8 * xcd + slot / nrb;
+            bx = slot % nrb;
+            g = pair % NKV;
+            sp = pair / NKV;
+        }
 #else
-    const int bx = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
+        bx = blockIdx.x;
+        g = blockIdx.y;
+        sp = blockIdx.z;
 #endif
+        sp_last = sp;
+        unit = 1;
+    } else {
+        const int pr = unit / NS;
+        sp = unit % NS;
+        sp_last = min(NS - 1, sp + (unit_end - unit) - 1);
+        g = pr / nrb;
+        bx = pr % nrb;
+        unit += sp_last - sp + 1;
+        if (seg > 0) __syncthreads();  // every wave is done with the previous segment's images
+    }
     const int row0 = bx * PF_ROWS;
     const int nrows = GRP * B;
     // last key any row of the workgroup sees, and this split's tiles [tb, tb + nt) of the row block's range
     const int last_row = min(row0 + PF_ROWS, nrows) - 1;
     const int kmax = p0 + last_row / GRP;
     const int n_tiles = kmax / PF_TILE + 1;
-    const int tb = sp * n_tiles / NS, nt = (sp + 1) * n_tiles / NS - tb;
+    const int tb = sp * n_tiles / NS, nt = (sp_last + 1) * n_tiles / NS - tb;
     const size_t rowbase = (size_t)g * kv.capacity;
     const int nvm = IMG ? PF_IMG_BYTES / 1024 / PF_WAVES : L::count(wave);
     uint32_t raw_lds[NBUF];
@@ -627,6 +674,7 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
         for (int dt = 0; dt < 16; dt++)
             dst[4 * dt] = pack16x4(o[rt][dt][0] * f, o[rt][dt][1] * f, o[rt][dt][2] * f, o[rt][dt][3] * f);
     }
+    }  // segments
     prof_end(prof);
 }
 
@@ -636,17 +684,22 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
 template <int NS>
 __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ gate, int nrows,
                                                     const PfPartO* __restrict__ part_o,
-                                                    const PfPartMl* __restrict__ part_ml, int ps,
+                                                    const PfPartMl* __restrict__ part_ml, int ps, int upw,
                                                     uint16_t* __restrict__ out16) {
     const int rr = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (rr >= nrows) return;
+    // the row's (KV head, row block) and, with upw > 1 units per workgroup, which of its split slots start a segment
+    // (k_prefill): split s does when s = 0 or its unit index is a multiple of upw
+    const int head = rr % NH, grow = (rr / NH) * GRP + head % GRP;
+    const int pr = (head / GRP) * ((GRP * (nrows / NH) + PF_ROWS - 1) / PF_ROWS) + grow / PF_ROWS;
     PfPartMl ml[NS];
     float4 ov[NS];
     float mx = -INFINITY;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
-        ml[s] = part_ml[(size_t)s * ps + rr];
-        ov[s] = unpack16x4(part_o[((size_t)s * ps + rr) * (HD / 4) + lane]);
+        const bool on = s == 0 || (pr * NS + s) % upw == 0;
+        ml[s] = on ? part_ml[(size_t)s * ps + rr] : make_float4(-INFINITY, 0.0f, 0.0f, 0.0f);
+        ov[s] = on ? unpack16x4(part_o[((size_t)s * ps + rr) * (HD / 4) + lane]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         mx = fmaxf(mx, ml[s].x);
     }
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -702,11 +755,13 @@ template <int KVT>
 static void launch_prefill_pass(const float* qp, const qwa_kv_layer& kv, int nb, int p0, const PfWork& w,
                                 hipStream_t st) {
     const int ns = pf_splits(nb);
-    const dim3 grid((GRP * nb + PF_ROWS - 1) / PF_ROWS, NKV, ns);
+    const int upw = pf_units_per_wg(nb, p0 + nb);
+    const int nrb = (GRP * nb + PF_ROWS - 1) / PF_ROWS, units = nrb * NKV * ns;
+    const dim3 grid = upw == 1 ? dim3(nrb, NKV, ns) : dim3((units + upw - 1) / upw);
     const ProfSlot ps = profile_slot(grid.x * grid.y * grid.z, st);
 #define QWA_PF_LAUNCH(N)                                                                                              \
     QWA_LAUNCH_MAIN(ps, (k_prefill<KVT, PF_IMAGE, N>), grid, dim3(PF_THREADS), st, qp, kv, nb, p0, w.img, w.tiles, \
-                    w.o, w.ml, w.ps)
+                    w.o, w.ml, w.ps, upw)
     if (ns == 5) QWA_PF_LAUNCH(5);
     else if (ns == 6) QWA_PF_LAUNCH(6);
     else if (ns == 7) QWA_PF_LAUNCH(7);
@@ -736,11 +791,12 @@ hipError_t launch_prefill(const float* q, const float* gate, const qwa_kv_layer&
         const float* gp = gate + (size_t)t0 * NH * HD;
         uint16_t* op = out16 + (size_t)t0 * NH * HD;
         const dim3 cg((nrows + 3) / 4), cb(256);
+        const int upw = pf_units_per_wg(nb, p0 + t0 + nb);
         switch (pf_splits(nb)) {
 #define QWA_PF_COMBINE(N) \
-    case N: hipLaunchKernelGGL(k_pf_combine<N>, cg, cb, 0, st, gp, nrows, w.o, w.ml, w.ps, op); break
+    case N: hipLaunchKernelGGL(k_pf_combine<N>, cg, cb, 0, st, gp, nrows, w.o, w.ml, w.ps, upw, op); break
             QWA_PF_COMBINE(5); QWA_PF_COMBINE(6); QWA_PF_COMBINE(7);
-            default: hipLaunchKernelGGL(k_pf_combine<PF_NS>, cg, cb, 0, st, gp, nrows, w.o, w.ml, w.ps, op); break;
+            default: hipLaunchKernelGGL(k_pf_combine<PF_NS>, cg, cb, 0, st, gp, nrows, w.o, w.ml, w.ps, upw, op); break;
 #undef QWA_PF_COMBINE
         }
     }
