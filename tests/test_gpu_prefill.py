@@ -16,7 +16,10 @@ from kvutil import KVTS, KV_NAMES, assert_close, dequant_cache, make_cache, seed
 
 pytestmark = pytest.mark.gpu
 
-CASES = [(0, 37), (0, 512), (300, 129), (1000, 500), (1480, 20), (200, 1300), (0, 420), (1100, 360)]
+# (100, 900) and (480, 1000) run their pass as workgroups of 3 (row block, KV head, split) units, 900 tokens with a last
+# workgroup of 2 units; (200, 1300) as a pass of 1024 such tokens and one of 276
+CASES = [(0, 37), (0, 512), (300, 129), (1000, 500), (1480, 20), (200, 1300), (0, 420), (1100, 360), (100, 900),
+         (480, 1000)]
 
 
 @pytest.fixture(scope="module", params=KVTS, ids=lambda k: KV_NAMES[k])
