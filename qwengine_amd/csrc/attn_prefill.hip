@@ -392,293 +392,296 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
     int unit = upw == 1 ? 0 : (int)blockIdx.x * upw;
     const int unit_end = upw == 1 ? 1 : min(unit + upw, units);
     for (int seg = 0; unit < unit_end; seg++) {
-    int bx, g, sp, sp_last;
-    if (upw == 1) {
+        int bx, g, sp, sp_last;
+        if (upw == 1) {
 #if QWA_PF_XCD
-        // XCD-aware numbering: workgroup lin is dispatched to XCD lin % 8; give each XCD whole (KV head, split) pairs,
-        // so the row blocks that read the same image tiles share one L2
-        // (a split count with NKV x NS not a multiple of 8 keeps the plain numbering)
-        bx = blockIdx.x;
-        g = blockIdx.y;
-        sp = blockIdx.z;
-        if constexpr ((NKV * NS) % 8 == 0) {
-            const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-            const int xcd = lin & 7, slot = lin >> 3;
-            const int pair = NKV * NS / 8 * xcd + slot / nrb;
-            bx = slot % nrb;
-            g = pair % NKV;
-            sp = pair / NKV;
-        }
+            // XCD-aware numbering: workgroup lin is dispatched to XCD lin % 8; give each XCD whole (KV head, split)
+            // pairs, so the row blocks that read the same image tiles share one L2
+            // (a split count with NKV x NS not a multiple of 8 keeps the plain numbering)
+            bx = blockIdx.x;
+            g = blockIdx.y;
+            sp = blockIdx.z;
+            if constexpr ((NKV * NS) % 8 == 0) {
+                const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+                const int xcd = lin & 7, slot = lin >> 3;
+                const int pair = NKV * NS / 8 * xcd + slot / nrb;
+                bx = slot % nrb;
+                g = pair % NKV;
+                sp = pair / NKV;
+            }
 #else
-        bx = blockIdx.x;
-        g = blockIdx.y;
-        sp = blockIdx.z;
+            bx = blockIdx.x;
+            g = blockIdx.y;
+            sp = blockIdx.z;
 #endif
-        sp_last = sp;
-        unit = 1;
-    } else {
-        const int pr = unit / NS;
-        sp = unit % NS;
-        sp_last = min(NS - 1, sp + (unit_end - unit) - 1);
-        g = pr / nrb;
-        bx = pr % nrb;
-        unit += sp_last - sp + 1;
-        if (seg > 0) __syncthreads();  // every wave is done with the previous segment's images
-    }
-    const int row0 = bx * PF_ROWS;
-    const int nrows = GRP * B;
-    // last key any row of the workgroup sees, and this split's tiles [tb, tb + nt) of the row block's range
-    const int last_row = min(row0 + PF_ROWS, nrows) - 1;
-    const int kmax = p0 + last_row / GRP;
-    const int n_tiles = kmax / PF_TILE + 1;
-    const int tb = sp * n_tiles / NS, nt = (sp_last + 1) * n_tiles / NS - tb;
-    const size_t rowbase = (size_t)g * kv.capacity;
-    const int nvm = IMG ? PF_IMG_BYTES / 1024 / PF_WAVES : L::count(wave);
-    uint32_t raw_lds[NBUF];
-#pragma unroll
-    for (int b = 0; b < NBUF; b++) raw_lds[b] = lds_addr(s_raw[b]);
-    const uint8_t* isrc = IMG ? img + (size_t)g * img_tiles * PF_IMG_BYTES : nullptr;
-
-    // this lane's rows (token r / 6, head r % 6) and last visible key qpos; Q / 16 as the fp16 B operand
-    int qpos[PF_RT];
-    h8 qb[PF_RT][8];
-    const int wrow0 = row0 + 16 * PF_RT * wave;
-#pragma unroll
-    for (int rt = 0; rt < PF_RT; rt++) {
-        const int r = wrow0 + 16 * rt + i16, tq = r / GRP, hh = r % GRP;
-        const bool valid = tq < B;
-        qpos[rt] = valid ? p0 + tq : -1;
-        const float* qrow = q + ((size_t)(valid ? tq : 0) * NH + g * GRP + hh) * HD;
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const float* src = qrow + 32 * s + 8 * lg;
-            const float4 a = *reinterpret_cast<const float4*>(src);
-            const float4 b = *reinterpret_cast<const float4*>(src + 4);
-            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            h8 v;
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = valid ? (_Float16)(x[k_perm<KVT>(j)] * 0.0625f) : (_Float16)0.0f;
-            qb[rt][s] = v;
+            sp_last = sp;
+            unit = 1;
+        } else {
+            const int pr = unit / NS;
+            sp = unit % NS;
+            sp_last = min(NS - 1, sp + (unit_end - unit) - 1);
+            g = pr / nrb;
+            bx = pr % nrb;
+            unit += sp_last - sp + 1;
+            if (seg > 0) __syncthreads();  // every wave is done with the previous segment's images
         }
-    }
-    // first query of the wave: tiles entirely at or before it need no causal mask
-    const int wave_qmin = p0 + wrow0 / GRP;
+        const int row0 = bx * PF_ROWS;
+        const int nrows = GRP * B;
+        // last key any row of the workgroup sees, and this split's tiles [tb, tb + nt) of the row block's range
+        const int last_row = min(row0 + PF_ROWS, nrows) - 1;
+        const int kmax = p0 + last_row / GRP;
+        const int n_tiles = kmax / PF_TILE + 1;
+        const int tb = sp * n_tiles / NS, nt = (sp_last + 1) * n_tiles / NS - tb;
+        const size_t rowbase = (size_t)g * kv.capacity;
+        const int nvm = IMG ? PF_IMG_BYTES / 1024 / PF_WAVES : L::count(wave);
+        uint32_t raw_lds[NBUF];
+#pragma unroll
+        for (int b = 0; b < NBUF; b++) raw_lds[b] = lds_addr(s_raw[b]);
+        const uint8_t* isrc = IMG ? img + (size_t)g * img_tiles * PF_IMG_BYTES : nullptr;
 
-    f4 o[PF_RT][16];
-    float m[PF_RT], l[PF_RT];
+        // this lane's rows (token r / 6, head r % 6) and last visible key qpos; Q / 16 as the fp16 B operand
+        int qpos[PF_RT];
+        h8 qb[PF_RT][8];
+        const int wrow0 = row0 + 16 * PF_RT * wave;
 #pragma unroll
-    for (int rt = 0; rt < PF_RT; rt++) {
-        m[rt] = -INFINITY;
-        l[rt] = 0.0f;
+        for (int rt = 0; rt < PF_RT; rt++) {
+            const int r = wrow0 + 16 * rt + i16, tq = r / GRP, hh = r % GRP;
+            const bool valid = tq < B;
+            qpos[rt] = valid ? p0 + tq : -1;
+            const float* qrow = q + ((size_t)(valid ? tq : 0) * NH + g * GRP + hh) * HD;
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++) o[rt][dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-
-    if (IMG && nt > 0) {
-        // prologue: images 0 .. AHEAD - 1 in flight, image 0 landed
-        wait_vmcnt<0>();  // the Q loads; from here on vmcnt counts only the tile loads
+            for (int s = 0; s < 8; s++) {
+                const float* src = qrow + 32 * s + 8 * lg;
+                const float4 a = *reinterpret_cast<const float4*>(src);
+                const float4 b = *reinterpret_cast<const float4*>(src + 4);
+                const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                h8 v;
 #pragma unroll
-        for (int i = 0; i < AHEAD; i++)
-            pf_issue_img(raw_lds[i], isrc + (size_t)(tb + min(i, nt - 1)) * PF_IMG_BYTES, wave, lane);
-        wait_vm(nvm * (AHEAD - 1));
-        __syncthreads();
-    } else if (nt > 0) {
-        // prologue: raw tiles 0 .. AHEAD - 1 in flight, tile 0 dequantised (and, with AHEAD >= 2, tile 1 landed)
-        wait_vmcnt<0>();  // the Q loads; from here on vmcnt counts only the tile loads
-#pragma unroll
-        for (int i = 0; i < L::AHEAD; i++)
-            pf_issue<KVT>(raw_lds[i], kv, rowbase, (tb + min(i, nt - 1)) * PF_TILE, kmax, wave, lane);
-        wait_vm(nvm * (L::AHEAD - 1));
-        __syncthreads();
-        pf_convert<KVT>(s_raw[0], s_k[0], s_vt[0], t);
-        if constexpr (L::AHEAD >= 2) wait_vm(nvm * (L::AHEAD - 2));
-        __syncthreads();
-    }
-
-    // The two waves of a SIMD (w and w + 4) run the phases of a tile in different orders so that one issues VALU /
-    // LDS work (dequantisation, softmax) while the other's MFMAs run:
-    //   waves 0-3: convert | S       | softmax | PV
-    //   waves 4-7: S       | softmax | PV      | convert
-    // With images there is no conversion and every wave runs S | softmax | PV.
-    const bool lead = (wave & PF_GROUP_BIT) == 0;
-    h8 pb[PF_RT];
-    auto pv = [&](const _Float16* Vt) {
-        h8 vf[PF_VD];
-        const _Float16* vrow = IMG ? Vt + i16 * PF_TILE + 8 * (lg ^ ((i16 >> 1) & 3)) : Vt + i16 * VT_LD + 8 * lg;
-        constexpr int vstep = IMG ? 16 * PF_TILE : 16 * VT_LD;
-#pragma unroll
-        for (int dt = 0; dt < PF_VD - 1; dt++) vf[dt] = lds_h8(vrow + vstep * dt);
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++) {
-            if (dt + PF_VD - 1 < 16) vf[(dt + PF_VD - 1) % PF_VD] = lds_h8(vrow + vstep * (dt + PF_VD - 1));
-#pragma unroll
-            for (int rt = 0; rt < PF_RT; rt++) o[rt][dt] = mfma16(vf[dt % PF_VD], pb[rt], o[rt][dt]);
+                for (int j = 0; j < 8; j++) v[j] = valid ? (_Float16)(x[k_perm<KVT>(j)] * 0.0625f) : (_Float16)0.0f;
+                qb[rt][s] = v;
+            }
         }
-    };
-    for (int i = 0; i < nt; i++) {
-        const int k0 = (tb + i) * PF_TILE, cur = i & 1;
-        // tile i + AHEAD (the last tile again near the end: a harmless re-read) into the raw buffer freed last
-        // iteration
-        if constexpr (IMG)
-            pf_issue_img(raw_lds[(i + AHEAD) % NBUF], isrc + (size_t)(tb + min(i + AHEAD, nt - 1)) * PF_IMG_BYTES,
-                         wave, lane);
-        else
-            pf_issue<KVT>(raw_lds[(i + AHEAD) % NBUF], kv, rowbase, (tb + min(i + AHEAD, nt - 1)) * PF_TILE, kmax,
-                          wave, lane);
-        const _Float16* Ks = IMG ? reinterpret_cast<const _Float16*>(s_raw[i % NBUF]) : s_k[cur];
-        const _Float16* Vt = IMG ? Ks + PF_IMG_K / 2 : s_vt[cur];
+        // first query of the wave: tiles entirely at or before it need no causal mask
+        const int wave_qmin = p0 + wrow0 / GRP;
 
-        // the next tile's raw bytes landed before the last barrier: dequantise them into the other fp16 tile
-        auto convert = [&]() {
-            if constexpr (!IMG && AHEAD >= 2) pf_convert<KVT>(s_raw[(i + 1) % NBUF], s_k[cur ^ 1], s_vt[cur ^ 1], t);
-        };
+        f4 o[PF_RT][16];
+        float m[PF_RT], l[PF_RT];
+#pragma unroll
+        for (int rt = 0; rt < PF_RT; rt++) {
+            m[rt] = -INFINITY;
+            l[rt] = 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < 16; dt++) o[rt][dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
 
-        f4 sc[PF_RT][PF_KT];
-        // image K operand bases: row i16, unit lg ^ (i16 & 3), s shifted by +-1 when bit 2 of i16 is set
-        const _Float16* kimg_e = Ks + i16 * HD + 8 * (lg ^ (i16 & 3)) + 32 * ((i16 >> 2) & 1);
-        const _Float16* kimg_o = kimg_e - 64 * ((i16 >> 2) & 1);
-        // ---- S^T = K Q^T for PF_KT key tiles of 16 (lane: key k0 + 16 k4 + 4 lg + i, row (rt, i16))
-        auto scores = [&]() {
+        if (IMG && nt > 0) {
+            // prologue: images 0 .. AHEAD - 1 in flight, image 0 landed
+            wait_vmcnt<0>();  // the Q loads; from here on vmcnt counts only the tile loads
 #pragma unroll
-            for (int k4 = 0; k4 < PF_KT; k4++)
-#pragma unroll
-                for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            // swizzled unit (4 s + lg) ^ x = 4 (s ^ (x >> 2)) + (lg ^ (x & 3)): two lane bases, even / odd s
-            auto kfrag = [&](int s, int k4) {
-                return IMG ? lds_h8((s & 1 ? kimg_o : kimg_e) + (16 * k4) * HD + 32 * s)
-                           : lds_h8(Ks + (16 * k4 + i16) * KS_LD + 8 * lg + 32 * s);
-            };
-            if constexpr (PF_KPF > 0) {
-                // the K fragments of step s + PF_KPF are read while step s multiplies (scheduling barriers keep the
-                // compiler from sinking the reads next to their MFMAs)
-                h8 kf[PF_KPF + 1][PF_KT];
-#pragma unroll
-                for (int s = 0; s < PF_KPF; s++)
-#pragma unroll
-                    for (int k4 = 0; k4 < PF_KT; k4++) kf[s][k4] = kfrag(s, k4);
-#pragma unroll
-                for (int s = 0; s < 8; s++) {
-                    if (s + PF_KPF < 8) {
-#pragma unroll
-                        for (int k4 = 0; k4 < PF_KT; k4++) kf[(s + PF_KPF) % (PF_KPF + 1)][k4] = kfrag(s + PF_KPF, k4);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int k4 = 0; k4 < PF_KT; k4++)
-#pragma unroll
-                        for (int rt = 0; rt < PF_RT; rt++)
-                            sc[rt][k4] = mfma16(kf[s % (PF_KPF + 1)][k4], qb[rt][s], sc[rt][k4]);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            } else {
-#pragma unroll
-                for (int s = 0; s < 8; s++) {
-#pragma unroll
-                    for (int k4 = 0; k4 < PF_KT; k4++) {
-                        const h8 a = kfrag(s, k4);
-#pragma unroll
-                        for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = mfma16(a, qb[rt][s], sc[rt][k4]);
-                    }
-                }
-            }
-        };
-
-        // ---- mask + online softmax.  The reference maximum m moves only when a score exceeds it by more than
-        // PF_RESCALE_T (probabilities stay <= e^PF_RESCALE_T, far inside fp16), so the accumulators are rarely
-        // rescaled.
-        auto softmax = [&]() {
-            const bool need_mask = k0 + PF_TILE - 1 > wave_qmin;
-            float cr[PF_RT];
-#pragma unroll
-            for (int rt = 0; rt < PF_RT; rt++) {
-                if (need_mask) {
-#pragma unroll
-                    for (int k4 = 0; k4 < PF_KT; k4++)
-#pragma unroll
-                        for (int j = 0; j < 4; j++) {
-                            const int key = k0 + 16 * k4 + 4 * lg + j;
-                            sc[rt][k4][j] = key > qpos[rt] ? -INFINITY : sc[rt][k4][j];
-                        }
-                }
-                float mx = -INFINITY;
-#pragma unroll
-                for (int k4 = 0; k4 < PF_KT; k4++)
-                    mx = max3f(max3f(mx, sc[rt][k4][0], sc[rt][k4][1]), sc[rt][k4][2], sc[rt][k4][3]);
-                mx = rows_max(mx);
-                const float mn = mx > m[rt] + PF_RESCALE_T ? mx : m[rt];
-                cr[rt] = mn == m[rt] ? 1.0f : fast_exp2((m[rt] - mn) * PF_LOG2E);  // m = -inf: c = 0
-                m[rt] = mn;
-                const float msl = mn == -INFINITY ? 0.0f : mn * PF_LOG2E;
-                // the row's lane sum of the fp16 probabilities themselves (the weights P.V applies), two per dot2
-                h8 p;
-#pragma unroll
-                for (int j = 0; j < 8; j++) p[j] = (_Float16)fast_exp2(fmaf(sc[rt][j >> 2][j & 3], PF_LOG2E, -msl));
-                const h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
-                float rs = __builtin_amdgcn_fdot2(h2{p[0], p[1]}, one2, 0.0f, false);
-                rs = __builtin_amdgcn_fdot2(h2{p[2], p[3]}, one2, rs, false);
-                rs = __builtin_amdgcn_fdot2(h2{p[4], p[5]}, one2, rs, false);
-                rs = __builtin_amdgcn_fdot2(h2{p[6], p[7]}, one2, rs, false);
-                pb[rt] = p;
-                l[rt] = l[rt] * cr[rt] + rs;
-            }
-            if (__any(cr[0] != 1.0f || cr[PF_RT - 1] != 1.0f)) {
-#pragma unroll
-                for (int rt = 0; rt < PF_RT; rt++)
-#pragma unroll
-                    for (int dt = 0; dt < 16; dt++) o[rt][dt] *= cr[rt];
-            }
-        };
-
-        if (!IMG && lead) convert();
-        scores();
-        softmax();
-        pv(Vt);
-        if (!IMG && !lead) convert();
-
-        if constexpr (IMG) {
-            // image i + 1 must have landed before the next iteration reads it; image i + 2 may stay in flight
+            for (int i = 0; i < AHEAD; i++)
+                pf_issue_img(raw_lds[i], isrc + (size_t)(tb + min(i, nt - 1)) * PF_IMG_BYTES, wave, lane);
             wait_vm(nvm * (AHEAD - 1));
             __syncthreads();
-        } else if constexpr (AHEAD >= 2) {
-            // tile i + 2 must have landed before the next iteration dequantises it; later tiles may stay in flight
-            wait_vm(nvm * (AHEAD - 2));
+        } else if (nt > 0) {
+            // prologue: raw tiles 0 .. AHEAD - 1 in flight, tile 0 dequantised (and, with AHEAD >= 2, tile 1 landed)
+            wait_vmcnt<0>();  // the Q loads; from here on vmcnt counts only the tile loads
+#pragma unroll
+            for (int i = 0; i < L::AHEAD; i++)
+                pf_issue<KVT>(raw_lds[i], kv, rowbase, (tb + min(i, nt - 1)) * PF_TILE, kmax, wave, lane);
+            wait_vm(nvm * (L::AHEAD - 1));
             __syncthreads();
-        } else {
-            wait_vm(0);
-            __syncthreads();
-            if (i + 1 < nt) pf_convert<KVT>(s_raw[(i + 1) % L::NBUF], s_k[cur ^ 1], s_vt[cur ^ 1], t);
+            pf_convert<KVT>(s_raw[0], s_k[0], s_vt[0], t);
+            if constexpr (L::AHEAD >= 2) wait_vm(nvm * (L::AHEAD - 2));
             __syncthreads();
         }
-    }
-    wait_vmcnt<0>();  // no direct-to-LDS load outlives the workgroup
 
-    // ---- partial state of this split: (m, l) and O / l; lane holds dims 16 dt + 4 lg + i of row (rt, i16)
+        // The two waves of a SIMD (w and w + 4) run the phases of a tile in different orders so that one issues VALU /
+        // LDS work (dequantisation, softmax) while the other's MFMAs run:
+        //   waves 0-3: convert | S       | softmax | PV
+        //   waves 4-7: S       | softmax | PV      | convert
+        // With images there is no conversion and every wave runs S | softmax | PV.
+        const bool lead = (wave & PF_GROUP_BIT) == 0;
+        h8 pb[PF_RT];
+        auto pv = [&](const _Float16* Vt) {
+            h8 vf[PF_VD];
+            const _Float16* vrow = IMG ? Vt + i16 * PF_TILE + 8 * (lg ^ ((i16 >> 1) & 3)) : Vt + i16 * VT_LD + 8 * lg;
+            constexpr int vstep = IMG ? 16 * PF_TILE : 16 * VT_LD;
 #pragma unroll
-    for (int rt = 0; rt < PF_RT; rt++) {
-        const float lt = rows_sum(l[rt]);
-        if (qpos[rt] < 0) continue;
-        const int r = wrow0 + 16 * rt + i16, rr = (r / GRP) * NH + g * GRP + r % GRP;
-        const size_t prow = (size_t)sp * ps + rr;
-        const float il = lt > 0.0f ? 1.0f / lt : 0.0f;  // a split that saw no key leaves l = 0 and O = 0
-        float amax = 0.0f;
+            for (int dt = 0; dt < PF_VD - 1; dt++) vf[dt] = lds_h8(vrow + vstep * dt);
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++)
+            for (int dt = 0; dt < 16; dt++) {
+                if (dt + PF_VD - 1 < 16) vf[(dt + PF_VD - 1) % PF_VD] = lds_h8(vrow + vstep * (dt + PF_VD - 1));
 #pragma unroll
-            for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(o[rt][dt][i]));
-        amax = rows_max(amax) * il;
-        const float qs = amax > 1e-30f ? 32767.0f / amax : 0.0f;  // (a row this small stores zeros: no inf scale)
-        const float f = il * qs;
-        if (lg == 0) part_ml[prow] = make_float4(m[rt], lt, qs > 0.0f ? amax * (1.0f / 32767.0f) : 0.0f, 0.0f);
-        PfPartO* dst = part_o + prow * (HD / 4) + lg;
+                for (int rt = 0; rt < PF_RT; rt++) o[rt][dt] = mfma16(vf[dt % PF_VD], pb[rt], o[rt][dt]);
+            }
+        };
+        for (int i = 0; i < nt; i++) {
+            const int k0 = (tb + i) * PF_TILE, cur = i & 1;
+            // tile i + AHEAD (the last tile again near the end: a harmless re-read) into the raw buffer freed last
+            // iteration
+            if constexpr (IMG)
+                pf_issue_img(raw_lds[(i + AHEAD) % NBUF], isrc + (size_t)(tb + min(i + AHEAD, nt - 1)) * PF_IMG_BYTES,
+                             wave, lane);
+            else
+                pf_issue<KVT>(raw_lds[(i + AHEAD) % NBUF], kv, rowbase, (tb + min(i + AHEAD, nt - 1)) * PF_TILE, kmax,
+                              wave, lane);
+            const _Float16* Ks = IMG ? reinterpret_cast<const _Float16*>(s_raw[i % NBUF]) : s_k[cur];
+            const _Float16* Vt = IMG ? Ks + PF_IMG_K / 2 : s_vt[cur];
+
+            // the next tile's raw bytes landed before the last barrier: dequantise them into the other fp16 tile
+            auto convert = [&]() {
+                if constexpr (!IMG && AHEAD >= 2)
+                    pf_convert<KVT>(s_raw[(i + 1) % NBUF], s_k[cur ^ 1], s_vt[cur ^ 1], t);
+            };
+
+            f4 sc[PF_RT][PF_KT];
+            // image K operand bases: row i16, unit lg ^ (i16 & 3), s shifted by +-1 when bit 2 of i16 is set
+            const _Float16* kimg_e = Ks + i16 * HD + 8 * (lg ^ (i16 & 3)) + 32 * ((i16 >> 2) & 1);
+            const _Float16* kimg_o = kimg_e - 64 * ((i16 >> 2) & 1);
+            // ---- S^T = K Q^T for PF_KT key tiles of 16 (lane: key k0 + 16 k4 + 4 lg + i, row (rt, i16))
+            auto scores = [&]() {
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++)
-            dst[4 * dt] = pack16x4(o[rt][dt][0] * f, o[rt][dt][1] * f, o[rt][dt][2] * f, o[rt][dt][3] * f);
-    }
+                for (int k4 = 0; k4 < PF_KT; k4++)
+#pragma unroll
+                    for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                // swizzled unit (4 s + lg) ^ x = 4 (s ^ (x >> 2)) + (lg ^ (x & 3)): two lane bases, even / odd s
+                auto kfrag = [&](int s, int k4) {
+                    return IMG ? lds_h8((s & 1 ? kimg_o : kimg_e) + (16 * k4) * HD + 32 * s)
+                               : lds_h8(Ks + (16 * k4 + i16) * KS_LD + 8 * lg + 32 * s);
+                };
+                if constexpr (PF_KPF > 0) {
+                    // the K fragments of step s + PF_KPF are read while step s multiplies (scheduling barriers keep the
+                    // compiler from sinking the reads next to their MFMAs)
+                    h8 kf[PF_KPF + 1][PF_KT];
+#pragma unroll
+                    for (int s = 0; s < PF_KPF; s++)
+#pragma unroll
+                        for (int k4 = 0; k4 < PF_KT; k4++) kf[s][k4] = kfrag(s, k4);
+#pragma unroll
+                    for (int s = 0; s < 8; s++) {
+                        if (s + PF_KPF < 8) {
+#pragma unroll
+                            for (int k4 = 0; k4 < PF_KT; k4++)
+                                kf[(s + PF_KPF) % (PF_KPF + 1)][k4] = kfrag(s + PF_KPF, k4);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int k4 = 0; k4 < PF_KT; k4++)
+#pragma unroll
+                            for (int rt = 0; rt < PF_RT; rt++)
+                                sc[rt][k4] = mfma16(kf[s % (PF_KPF + 1)][k4], qb[rt][s], sc[rt][k4]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 8; s++) {
+#pragma unroll
+                        for (int k4 = 0; k4 < PF_KT; k4++) {
+                            const h8 a = kfrag(s, k4);
+#pragma unroll
+                            for (int rt = 0; rt < PF_RT; rt++) sc[rt][k4] = mfma16(a, qb[rt][s], sc[rt][k4]);
+                        }
+                    }
+                }
+            };
+
+            // ---- mask + online softmax.  The reference maximum m moves only when a score exceeds it by more than
+            // PF_RESCALE_T (probabilities stay <= e^PF_RESCALE_T, far inside fp16), so the accumulators are rarely
+            // rescaled.
+            auto softmax = [&]() {
+                const bool need_mask = k0 + PF_TILE - 1 > wave_qmin;
+                float cr[PF_RT];
+#pragma unroll
+                for (int rt = 0; rt < PF_RT; rt++) {
+                    if (need_mask) {
+#pragma unroll
+                        for (int k4 = 0; k4 < PF_KT; k4++)
+#pragma unroll
+                            for (int j = 0; j < 4; j++) {
+                                const int key = k0 + 16 * k4 + 4 * lg + j;
+                                sc[rt][k4][j] = key > qpos[rt] ? -INFINITY : sc[rt][k4][j];
+                            }
+                    }
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (int k4 = 0; k4 < PF_KT; k4++)
+                        mx = max3f(max3f(mx, sc[rt][k4][0], sc[rt][k4][1]), sc[rt][k4][2], sc[rt][k4][3]);
+                    mx = rows_max(mx);
+                    const float mn = mx > m[rt] + PF_RESCALE_T ? mx : m[rt];
+                    cr[rt] = mn == m[rt] ? 1.0f : fast_exp2((m[rt] - mn) * PF_LOG2E);  // m = -inf: c = 0
+                    m[rt] = mn;
+                    const float msl = mn == -INFINITY ? 0.0f : mn * PF_LOG2E;
+                    // the row's lane sum of the fp16 probabilities themselves (the weights P.V applies), two per dot2
+                    h8 p;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) p[j] = (_Float16)fast_exp2(fmaf(sc[rt][j >> 2][j & 3], PF_LOG2E, -msl));
+                    const h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+                    float rs = __builtin_amdgcn_fdot2(h2{p[0], p[1]}, one2, 0.0f, false);
+                    rs = __builtin_amdgcn_fdot2(h2{p[2], p[3]}, one2, rs, false);
+                    rs = __builtin_amdgcn_fdot2(h2{p[4], p[5]}, one2, rs, false);
+                    rs = __builtin_amdgcn_fdot2(h2{p[6], p[7]}, one2, rs, false);
+                    pb[rt] = p;
+                    l[rt] = l[rt] * cr[rt] + rs;
+                }
+                if (__any(cr[0] != 1.0f || cr[PF_RT - 1] != 1.0f)) {
+#pragma unroll
+                    for (int rt = 0; rt < PF_RT; rt++)
+#pragma unroll
+                        for (int dt = 0; dt < 16; dt++) o[rt][dt] *= cr[rt];
+                }
+            };
+
+            if (!IMG && lead) convert();
+            scores();
+            softmax();
+            pv(Vt);
+            if (!IMG && !lead) convert();
+
+            if constexpr (IMG) {
+                // image i + 1 must have landed before the next iteration reads it; image i + 2 may stay in flight
+                wait_vm(nvm * (AHEAD - 1));
+                __syncthreads();
+            } else if constexpr (AHEAD >= 2) {
+                // tile i + 2 must have landed before the next iteration dequantises it; later tiles may stay in flight
+                wait_vm(nvm * (AHEAD - 2));
+                __syncthreads();
+            } else {
+                wait_vm(0);
+                __syncthreads();
+                if (i + 1 < nt) pf_convert<KVT>(s_raw[(i + 1) % L::NBUF], s_k[cur ^ 1], s_vt[cur ^ 1], t);
+                __syncthreads();
+            }
+        }
+        wait_vmcnt<0>();  // no direct-to-LDS load outlives the workgroup
+
+        // ---- partial state of this split: (m, l) and O / l; lane holds dims 16 dt + 4 lg + i of row (rt, i16)
+#pragma unroll
+        for (int rt = 0; rt < PF_RT; rt++) {
+            const float lt = rows_sum(l[rt]);
+            if (qpos[rt] < 0) continue;
+            const int r = wrow0 + 16 * rt + i16, rr = (r / GRP) * NH + g * GRP + r % GRP;
+            const size_t prow = (size_t)sp * ps + rr;
+            const float il = lt > 0.0f ? 1.0f / lt : 0.0f;  // a split that saw no key leaves l = 0 and O = 0
+            float amax = 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < 16; dt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(o[rt][dt][i]));
+            amax = rows_max(amax) * il;
+            const float qs = amax > 1e-30f ? 32767.0f / amax : 0.0f;  // (a row this small stores zeros: no inf scale)
+            const float f = il * qs;
+            if (lg == 0) part_ml[prow] = make_float4(m[rt], lt, qs > 0.0f ? amax * (1.0f / 32767.0f) : 0.0f, 0.0f);
+            PfPartO* dst = part_o + prow * (HD / 4) + lg;
+#pragma unroll
+            for (int dt = 0; dt < 16; dt++)
+                dst[4 * dt] = pack16x4(o[rt][dt][0] * f, o[rt][dt][1] * f, o[rt][dt][2] * f, o[rt][dt][3] * f);
+        }
     }  // segments
     prof_end(prof);
 }
 
-// Merges the partial states of the ns splits of each output row in split order, applies the sigmoid gate and writes fp16: one
+// Merges the partial states of the ns splits of each output row in split order (the slots that start a segment, see
+// k_prefill), applies the sigmoid gate and writes fp16: one
 // wave per row (token * NH + head), 4 dims per lane.  Split s weighs w_s = l_s exp(m_s - M); the row's output is
 // sum_s w_s (O_s / l_s) / sum_s w_s.
 template <int NS>
