@@ -681,9 +681,8 @@ k_prefill(const float* __restrict__ q, qwa_kv_layer kv, int B, int p0, const uin
 }
 
 // Merges the partial states of the ns splits of each output row in split order (the slots that start a segment, see
-// k_prefill), applies the sigmoid gate and writes fp16: one
-// wave per row (token * NH + head), 4 dims per lane.  Split s weighs w_s = l_s exp(m_s - M); the row's output is
-// sum_s w_s (O_s / l_s) / sum_s w_s.
+// k_prefill), applies the sigmoid gate and writes fp16: one wave per row (token * NH + head), 4 dims per lane.
+// Split s weighs w_s = l_s exp(m_s - M); the row's output is sum_s w_s (O_s / l_s) / sum_s w_s.
 template <int NS>
 __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ gate, int nrows,
                                                     const PfPartO* __restrict__ part_o,
