@@ -14,11 +14,13 @@
 //    LDS instead and all threads dequantise the next tile cooperatively inside the loop;
 //  * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16 (fp32 accumulation); P^T comes out of the S^T
 //    accumulator already in B-operand layout; online softmax in fp32 with a lazy rescale;
-//  * the causal key range of a row block is cut into fixed splits (pf_splits, one workgroup each) so that the
-//    24 row blocks x 4 KV heads of a 1024-token chunk fill the chip; each split leaves a partial state (m, l, O / l)
-//    in the caller's workspace and k_pf_combine merges the splits in a fixed order, applies the sigmoid gate and
-//    writes fp16.  Chunks longer than PF_MAXB tokens run as several passes.  Nothing here allocates: the images
-//    and partial states live in a workspace of prefill_work_bytes(B, p0 + B) bytes.
+//  * the causal key range of a row block is cut into fixed splits (pf_splits) so that the 24 row blocks x 4 KV
+//    heads of a 1024-token chunk fill the chip; the (row block, KV head, split) units run one per workgroup, or, for
+//    a 1024-token pass, three consecutive ones per workgroup in a single round (pf_units_per_wg), a run of splits of
+//    one row block being walked as one key range.  Each run leaves a partial state (m, l, O / l) in the caller's
+//    workspace and k_pf_combine merges them in a fixed order, applies the sigmoid gate and writes fp16.  Chunks
+//    longer than PF_MAXB tokens run as several passes.  Nothing here allocates: the images and partial states live
+//    in a workspace of prefill_work_bytes(B, p0 + B) bytes.
 #include <float.h>
 
 #include "kv_operands.hpp"
