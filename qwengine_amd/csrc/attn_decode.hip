@@ -56,6 +56,12 @@ static __device__ unsigned long long dec_wtrace[4096][16];
 
 constexpr int REC = 260;    // partial record: m, l, 2 pad, O[256] (16-byte aligned O)
 constexpr int CGRP = 16;    // combine: records per fixed summation group
+#ifndef QWA_DEC3H
+#define QWA_DEC3H 1
+#endif
+#ifndef QWA_DEC3H_CHAIN
+#define QWA_DEC3H_CHAIN 1
+#endif
 #ifndef QWA_Q4_CHAIN_FROM
 #define QWA_Q4_CHAIN_FROM 24576
 #endif
@@ -280,8 +286,9 @@ __device__ __forceinline__ void merge_split(MergeLdsN<WGW>& s, int wave, int lan
 }
 
 // merge_split in two rounds of 8 dimension tiles, for workgroups whose LDS holds only half of MergeLdsN: round h
-// exchanges tiles 8 h .. 8 h + 7, which waves 4 h .. 4 h + 3 own (wave w still owns tiles 2 w and 2 w + 1).  Every
-// fold is merge_split's, on the same values in the same order, so the results are bit-identical.
+// exchanges tiles 8 h .. 8 h + 7, which the waves of half h of the workgroup own (wave w still owns tiles TPW w ..
+// TPW w + TPW - 1).  Every fold is merge_split's, on the same values in the same order, so the results are
+// bit-identical.
 template <int WGW>
 struct MergeLdsH {
     f4 o[WGW][8][64];
@@ -291,8 +298,9 @@ struct MergeLdsH {
 template <int WGW>
 __device__ __forceinline__ void merge_split_half(MergeLdsH<WGW>& s, int wave, int lane, float& m, float& l,
                                                  const f4* o, f4* om) {
-    static_assert(WGW == 8, "two rounds of 8 tiles: 4 owner waves of 2 tiles each per round");
+    static_assert(WGW == 8 || WGW == 4, "two rounds of 8 tiles, owned by half of the waves each");
     constexpr int TPW = 16 / WGW;
+    constexpr int OWN = WGW / 2;  // owner waves per round
     l = half4_sum(l);
     const float m_in = m, l_in = l;
 #pragma unroll
@@ -305,7 +313,7 @@ __device__ __forceinline__ void merge_split_half(MergeLdsH<WGW>& s, int wave, in
             s.ml[wave][1][lane] = l_in;
         }
         __syncthreads();
-        if ((wave >> 2) == h) {
+        if (wave / OWN == h) {
             float mm[WGW], ll[WGW];
             f4 oo[WGW][TPW];
 #pragma unroll
@@ -313,7 +321,7 @@ __device__ __forceinline__ void merge_split_half(MergeLdsH<WGW>& s, int wave, in
                 mm[w] = s.ml[w][0][lane];
                 ll[w] = s.ml[w][1][lane];
 #pragma unroll
-                for (int t = 0; t < TPW; t++) oo[w][t] = s.o[w][TPW * (wave - 4 * h) + t][lane];
+                for (int t = 0; t < TPW; t++) oo[w][t] = s.o[w][TPW * (wave - OWN * h) + t][lane];
             }
 #pragma unroll
             for (int step = 1; step < WGW; step *= 2)
@@ -416,6 +424,29 @@ struct DecChainLds {
     } v;
     int prog[WGW];
 };
+// LDS of the one-round three-tile verify (k_dec3h): the Q fragments of the three tiles, kept for both half records,
+// and the rings and half of the merge exchange beside them, so the second half's first chunks load while the first
+// half merges (in two rounds); the second half merges over rings and exchange together.
+template <int KVT>
+struct DecHalvesLds {
+    using C = ChunkLds<KVT>;
+    static_assert(DecCfg<KVT, 3>::NST == 1, "one ring slot");
+    h8 q[3 * 8 * 2 * 64];
+    union {
+        struct {
+            uint8_t ring[4][1][C::BYTES];
+            MergeLdsH<4> merge;
+        } a;
+        MergeLdsN<4> merge;
+    } u;
+    __device__ h8* qf() { return q; }
+    __device__ h8* qf_next() { return nullptr; }
+    __device__ uint8_t (*rings(int w))[C::BYTES] { return u.a.ring[w]; }
+    __device__ int* progs() { return nullptr; }
+    __device__ MergeLdsN<4>& mg() { return u.merge; }
+    __device__ MergeLdsH<4>& mg_half() { return u.a.merge; }
+};
+
 template <int KVT, int RT, int WGW>
 struct DecChainView {
     using C = ChunkLds<KVT>;
@@ -431,7 +462,9 @@ struct DecChainView {
 
 // One workgroup (record rec of KV head g) of the F16 / Q8_0 decode; its LDS is s.  CHAIN as in dec4_body: 1 for the
 // first of two chained passes (it stages the second's Q fragments, issues the second's first chunk once its own loop
-// is done, and merges in two rounds), 2 for the second; the arithmetic of a row is that of CHAIN = 0.
+// is done, and merges in two rounds), 2 for the second; 3 and 4 the same for the two half records rec, rec + 1 of
+// k_dec3h (the same row tiles, so the Q fragments stay; the second half's classes are the next ones).  The arithmetic
+// of a row is that of CHAIN = 0.
 template <int KVT, int RT, int WGW, int WPE, int CHAIN = 0, class LDS = DecLds<KVT, RT, WGW, WPE>>
 __device__ __forceinline__ void dec_body(LDS& s, const float* __restrict__ q, const qwa_kv_layer& kv, int pos0,
                                          int nq, int rt0, float* __restrict__ work, int rec, int g,
@@ -440,7 +473,7 @@ __device__ __forceinline__ void dec_body(LDS& s, const float* __restrict__ q, co
     using C = ChunkLds<KVT>;
     constexpr int NST = DecCfg<KVT, RT>::NST;
     constexpr bool QLDS = RT > 1;
-    constexpr bool PRIO = CHAIN != 0 || DecLds<KVT, RT, WGW, WPE>::PRIO;
+    constexpr bool PRIO = CHAIN == 1 || CHAIN == 2 || (CHAIN == 0 && DecLds<KVT, RT, WGW, WPE>::PRIO);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
     const int i16 = lane & 15, lg = lane >> 4;
     const int kmax = pos0 + nq - 1;
@@ -464,7 +497,7 @@ __device__ __forceinline__ void dec_body(LDS& s, const float* __restrict__ q, co
     const uint32_t koff = chunk_koff<KVT>(lane);
     auto issue = [&](uint8_t* dst, int kb) { issue_chunk<KVT>(dst, kv, rowbase, kb, kmax, lane, koff); };
     // the ring's loads go out before the Q set-up, so their HBM latency overlaps it
-    if (CHAIN != 2 && nmine > 0) {
+    if (CHAIN != 2 && CHAIN != 4 && nmine > 0) {
 #pragma unroll
         for (int st = 0; st < NST; st++) issue(ring[st], chunk_key(st));
     }
@@ -472,7 +505,7 @@ __device__ __forceinline__ void dec_body(LDS& s, const float* __restrict__ q, co
     // Q / 16 as fp16 hi + lo parts, B operand of block b: lane (row i16, group lg) holds dims 32 b + 8 lg + perm(j);
     // the fragments are loaded once per workgroup through LDS
     h8* s_q = s.qf();
-    if constexpr (CHAIN != 2) q_frags_to_lds<KVT, RT>(q, nq, g, rt0, s_q);
+    if constexpr (CHAIN != 2 && CHAIN != 4) q_frags_to_lds<KVT, RT>(q, nq, g, rt0, s_q);
     if constexpr (CHAIN == 1) q_frags_to_lds<KVT, 1>(q, nq, g, rt0 + RT, s.qf_next());
     __syncthreads();
     TRACE(1);
@@ -633,6 +666,12 @@ __device__ __forceinline__ void dec_body(LDS& s, const float* __restrict__ q, co
             for (int st = 0; st < NST; st++) issue(ring[st], chunk_key(st));
         }
     }
+    if constexpr (CHAIN == 3) {
+        // the next half record's class of this wave (as cls above, for rec + 1), whose first chunk loads while this
+        // half merges
+        const int cn = (rec + 1) >> 1 == rec >> 1 ? (rec >> 1) + R * (WGW * ((rec + 1) & 1) + wave) : -1;
+        if (cn >= 0 && cn < nchunk) issue(ring[0], CHUNK * cn);
+    }
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     TRACE(3);
 
@@ -643,7 +682,7 @@ __device__ __forceinline__ void dec_body(LDS& s, const float* __restrict__ q, co
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         f4 om[TPW];
-        if constexpr (CHAIN == 1) merge_split_half<WGW>(s.mg_half(), wave, lane, m[rt], l[rt], o[rt], om);
+        if constexpr (CHAIN == 1 || CHAIN == 3) merge_split_half<WGW>(s.mg_half(), wave, lane, m[rt], l[rt], o[rt], om);
         else merge_split<WGW>(s.mg(), wave, lane, m[rt], l[rt], o[rt], om);
         const int r = 16 * (rt0 + rt) + i16;
         const int qt = r / GRP, hh = r % GRP;
@@ -676,6 +715,29 @@ k_dec(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, f
       unsigned long long* prof) {
     __shared__ __attribute__((aligned(16))) DecLds<KVT, RT, WGW, WPE> s;
     dec_body<KVT, RT, WGW, WPE>(s, q, kv, pos0, nq, rt0, work, blockIdx.x, blockIdx.y, prof);
+}
+
+// The one-pass three-tile verify with both half records of record blockIdx.x in one workgroup, one after the other
+// (grid (records, NKV): one round of the chip instead of two; each half is exactly k_dec<KVT, 3, 4, 1>'s code)
+template <int KVT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+k_dec3h(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0, float* __restrict__ work,
+        unsigned long long* prof) {
+#if QWA_DEC3H_CHAIN
+    // the second half's first chunks load while the first half merges; the Q fragments serve both halves
+    __shared__ __attribute__((aligned(16))) DecHalvesLds<KVT> s;
+    prof_start(prof);
+    dec_body<KVT, 3, 4, 1, 3>(s, q, kv, pos0, nq, rt0, work, 2 * blockIdx.x, blockIdx.y, nullptr);
+    dec_body<KVT, 3, 4, 1, 4>(s, q, kv, pos0, nq, rt0, work, 2 * blockIdx.x + 1, blockIdx.y, nullptr);
+    prof_end(prof);
+#else
+    __shared__ __attribute__((aligned(16))) DecLds<KVT, 3, 4, 1> s;
+    prof_start(prof);
+    dec_body<KVT, 3, 4, 1>(s, q, kv, pos0, nq, rt0, work, 2 * blockIdx.x, blockIdx.y, nullptr);
+    __syncthreads();  // the first half's merge reads are done before the second half's chunks land in LDS
+    dec_body<KVT, 3, 4, 1>(s, q, kv, pos0, nq, rt0, work, 2 * blockIdx.x + 1, blockIdx.y, nullptr);
+    prof_end(prof);
+#endif
 }
 
 // The two passes of a three-tile verify in one launch, grid (records, NKV): every workgroup runs the pass of row
@@ -1221,6 +1283,8 @@ k_dec4_3(const float* __restrict__ q, qwa_kv_layer kv, int pos0, int nq, int rt0
 // arithmetic, so the bits are those of any other build.  (Trace builds instantiate it here.)
 extern template __global__ void k_dec<QWA_KV_F16, 3, 4, 1>(const float* __restrict__, qwa_kv_layer, int, int, int,
                                                            float* __restrict__, unsigned long long*);
+extern template __global__ void k_dec3h<QWA_KV_F16>(const float* __restrict__, qwa_kv_layer, int, int, int,
+                                                    float* __restrict__, unsigned long long*);
 #endif
 
 #ifndef QWA_DEC_KERNELS_ONLY
@@ -1352,10 +1416,10 @@ constexpr int DEC_WGW = WG_CLASSES;
 // 6..8-query verify in two passes (two tiles, one tile): both as one launch
 constexpr bool ONE_LAUNCH = QWA_ONE_LAUNCH != 0;
 #ifndef QWA_Q8_ONEPASS
-#define QWA_Q8_ONEPASS 212992
+#define QWA_Q8_ONEPASS 147456
 #endif
 #ifndef QWA_F16_ONEPASS
-#define QWA_F16_ONEPASS 24576
+#define QWA_F16_ONEPASS 12288
 #endif
 #ifndef QWA_DEC3
 #define QWA_DEC3 1
@@ -1379,7 +1443,10 @@ static bool dec3_pass(bool three, const float* q, const qwa_kv_layer& kv, int po
                       float* work, const ProfSlot& ps, hipStream_t st) {
     if constexpr (KVT != QWA_KV_Q4_0) {
         if (three) {
-            QWA_LAUNCH_MAIN(ps, (k_dec<KVT, 3, 4, 1>), dim3(2 * nrec, NKV), dim3(256), st, q, kv, pos0, nq, t, work);
+            if (QWA_DEC3H)
+                QWA_LAUNCH_MAIN(ps, (k_dec3h<KVT>), dim3(nrec, NKV), dim3(256), st, q, kv, pos0, nq, t, work);
+            else
+                QWA_LAUNCH_MAIN(ps, (k_dec<KVT, 3, 4, 1>), dim3(2 * nrec, NKV), dim3(256), st, q, kv, pos0, nq, t, work);
             return true;
         }
     }

@@ -10,5 +10,7 @@ namespace qwa {
 #ifndef QWA_TRACE
 template __global__ void k_dec<QWA_KV_F16, 3, 4, 1>(const float* __restrict__, qwa_kv_layer, int, int, int,
                                                     float* __restrict__, unsigned long long*);
+template __global__ void k_dec3h<QWA_KV_F16>(const float* __restrict__, qwa_kv_layer, int, int, int,
+                                             float* __restrict__, unsigned long long*);
 #endif
 }  // namespace qwa
