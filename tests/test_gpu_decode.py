@@ -108,6 +108,28 @@ def test_verify_chained_passes_bit_identical(gpu, oracle, kvt, nq):
             assert np.array_equal(out[t].view(np.uint32), alone[0].view(np.uint32)), (end, t)
 
 
+@pytest.mark.parametrize("kvt,nq", [(ops.F16, 7), (ops.F16, 6), (ops.Q8_0, 8)], ids=["f16-nq7", "f16-nq6", "q8_0-nq8"])
+def test_verify_one_pass_boundary(gpu, oracle, kvt, nq):
+    """F16 / Q8_0 verify with 6..8 queries takes the one-pass three-tile kernel (both half records of a record in one
+    workgroup) from 12288 / 147456 covered positions on, the two passes in one launch below.  Calls that end on
+    either side of that boundary give every query the bits of the same query decoded alone, and the oracle's
+    values."""
+    print(f"verify one-pass boundary kvt={KV_NAMES[kvt]} nq={nq}", flush=True)
+    bound = 12288 if kvt == ops.F16 else 147456
+    n_pos = bound + 8
+    kv, _, _ = make_cache(kvt, n_pos, n_pos, seed=50 + nq)
+    q, gate = _qg(nq, 97 + nq)
+    Kd, Vd = dequant_cache(kv, n_pos)
+    for end in (bound - 1, bound, bound + 8):  # positions the call covers: pos0 + nq
+        pos0 = end - nq
+        out = _decode(kv, q, gate, pos0, nq).cpu().numpy()
+        ref = oracle.attention(q.cpu().numpy(), gate.cpu().numpy(), Kd, Vd, pos0, nq)
+        assert_close(out, ref, f"verify {KV_NAMES[kvt]} nq={nq} end={end}")
+        for t in range(nq):
+            alone = _decode(kv, q[t:t + 1].contiguous(), gate[t:t + 1].contiguous(), pos0 + t, 1).cpu().numpy()
+            assert np.array_equal(out[t].view(np.uint32), alone[0].view(np.uint32)), (end, t)
+
+
 @pytest.mark.parametrize("kvt", KVTS, ids=lambda k: KV_NAMES[k])
 def test_decode_multi_is_bit_identical_to_single_calls(gpu, kvt):
     """decode_batch(n) == n x decode(), bit for bit (src/cuda/ops.cuh:134-135); split boundaries crossed on purpose."""
