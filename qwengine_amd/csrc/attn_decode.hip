@@ -1311,6 +1311,9 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
     const size_t sstride = (size_t)NKV * MAXQ * GRP * REC;
     const float* base = work + (((size_t)g * MAXQ + t) * GRP + hh) * REC;
     const int d = 64 * quarter + dim;
+    const size_t o = ((size_t)t * NH + h) * HD + d;
+    // the gate of slice 0's output, loaded with the records (not one memory round trip after them)
+    const float gv = slice == 0 ? gate[o] : 0.0f;
 
     // every load up front: this thread's O values (groups slice, slice + 4, ...) and one record's (m, l)
     float ov[GPS][CGRP], ov2[GPS][CGRP];
@@ -1383,8 +1386,7 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ w
         L += s_gl[gr];
         A += s_ga[gr][dim];
     }
-    const size_t o = ((size_t)t * NH + h) * HD + d;
-    const float v = (A / L) * sigmoid(gate[o]);
+    const float v = (A / L) * sigmoid(gv);
     out[o] = v;
     if (out_host) {
         out_host[o] = v;
