@@ -356,3 +356,28 @@ def test_profile_window_stamps(gpu):
     assert ms >= dev_ms > 0.0
     assert 500.0 < mhz < 3500.0
     assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("kvt", KVTS, ids=lambda k: KV_NAMES[k])
+def test_decode_verify_random_sweep(gpu, oracle, kvt):
+    """Seeded random calls over one cache of 40968 positions, spanning every route below it (one-tile decode, two-tile
+    pass, the two passes unchained and chained, the one-pass three-tile kernel for F16): nq in 1..8 and a random end.
+    Each call gives every query the bits of the same query decoded alone (the nq-independence contract), and its last
+    query the oracle's values."""
+    n_pos = 40968
+    rng = np.random.default_rng(1234 + kvt)
+    kv, _, _ = make_cache(kvt, n_pos, n_pos, seed=60 + kvt)
+    Kd, Vd = dequant_cache(kv, n_pos)
+    for case in range(40):
+        nq = int(rng.integers(1, 9))
+        end = int(rng.integers(nq, n_pos + 1)) if case % 2 else int(rng.integers(nq, 4096))  # positions covered
+        pos0 = end - nq
+        print(f"random sweep kvt={KV_NAMES[kvt]} case={case} nq={nq} pos0={pos0}", flush=True)
+        q, gate = _qg(nq, 500 + 10 * case + kvt)
+        out = _decode(kv, q, gate, pos0, nq).cpu().numpy()
+        for t in range(nq):
+            alone = _decode(kv, q[t:t + 1].contiguous(), gate[t:t + 1].contiguous(), pos0 + t, 1).cpu().numpy()
+            assert np.array_equal(out[t].view(np.uint32), alone[0].view(np.uint32)), (case, nq, pos0, t)
+        ql, gl = q[nq - 1:].cpu().numpy(), gate[nq - 1:].cpu().numpy()
+        ref = oracle.attention(ql, gl, Kd, Vd, pos0 + nq - 1, 1)
+        assert_close(out[nq - 1:], ref, f"random sweep {KV_NAMES[kvt]} nq={nq} pos0={pos0}")

@@ -317,3 +317,27 @@ def test_prefill_at_max_positions(gpu, oracle):
     qn, gn = q.cpu().numpy(), gate.cpu().numpy()
     refs = np.stack([oracle.attention(qn[t:t + 1], gn[t:t + 1], Kd, Vd, p0 + t, 1)[0] for t in ts])
     assert_close(got[ts], refs, "prefill ending at 262144")
+
+
+@pytest.mark.parametrize("kvt", KVTS, ids=lambda k: KV_NAMES[k])
+def test_prefill_random_sweep(gpu, oracle, kvt):
+    """Seeded random chunks (p0, B) over one cache of 20000 positions, B in 1..1400 (one or two passes, 5 to 8 splits,
+    units grouped per workgroup or not): every row against the FP32 test kernel (the reference's bound), the first and
+    last 8 rows against the oracle."""
+    n_pos = 20000
+    rng = np.random.default_rng(4321 + kvt)
+    kv, _, _ = make_cache(kvt, n_pos, n_pos, seed=80 + kvt)
+    Kd, Vd = dequant_cache(kv, n_pos)
+    for case in range(12):
+        B = int(rng.integers(1, 1401))
+        p0 = int(rng.integers(0, n_pos - B + 1))
+        print(f"prefill random sweep kvt={KV_NAMES[kvt]} case={case} p0={p0} B={B}", flush=True)
+        q = seeded_normal((B, 24, 256), 700 + 10 * case + kvt)
+        gate = seeded_normal((B, 24, 256), 705 + 10 * case + kvt)
+        got = _prefill(ops.attn_prefill, kv, q, gate, B, p0)
+        simple = _prefill(ops.attn_prefill_simple, kv, q, gate, B, p0)
+        assert np.abs(got - simple).max() / np.abs(simple).max() < 5e-3, (case, p0, B)
+        for r0 in sorted({0, max(0, B - 8)}):
+            nr = min(8, B - r0)
+            ref = oracle.attention(q[r0:r0 + nr].cpu().numpy(), gate[r0:r0 + nr].cpu().numpy(), Kd, Vd, p0 + r0, nr)
+            assert_close(got[r0:r0 + nr], ref, f"prefill random {KV_NAMES[kvt]} p0={p0} B={B} rows {r0}..")
