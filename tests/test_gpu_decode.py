@@ -266,12 +266,14 @@ def test_decode_calls_on_two_streams(gpu):
             assert torch.equal(o, w), rep
 
 
-@pytest.mark.parametrize("kvt,n,nq", [(ops.Q4_0, 9000, 3), (ops.Q4_0, 9000, 7), (ops.F16, 33000, 7)],
-                         ids=["q4_0-nq3", "q4_0-nq7-one-launch", "f16-nq7-three-tiles"])
+@pytest.mark.parametrize("kvt,n,nq", [(ops.Q4_0, 9000, 3), (ops.Q4_0, 9000, 7), (ops.F16, 33000, 7),
+                                      (ops.Q4_0, 30000, 7), (ops.Q8_0, 20000, 8)],
+                         ids=["q4_0-nq3", "q4_0-nq7-one-launch", "f16-nq7-three-tiles", "q4_0-nq7-chained",
+                              "q8_0-nq8-chained"])
 def test_decode_in_hip_graph(gpu, kvt, n, nq):
     """A decode step captured into a HIP graph (the engine's decode step): every replay, with eager decode calls in
-    between, gives the eager bits; also the verify routes of 6..8 queries (two passes in one launch, the one-pass
-    three-tile kernel with half records)."""
+    between, gives the eager bits; also the verify routes of 6..8 queries (two passes in one launch, unchained and
+    chained, and the one-pass three-tile kernel with both half records in one workgroup)."""
     print(f"graph kvt={KV_NAMES[kvt]} n={n} nq={nq}", flush=True)
     kv, _, _ = make_cache(kvt, n + nq, n + nq, seed=61)
     q, gate = _qg(nq, 63)
