@@ -1426,15 +1426,13 @@ constexpr bool ONE_LAUNCH = QWA_ONE_LAUNCH != 0;
 #ifndef QWA_DEC3
 #define QWA_DEC3 1
 #endif
-// Three row tiles (6..8 queries) in one pass at one wave per SIMD, against the two passes (two tiles, one tile) as
-// one launch; 7 queries, us per layer, one pass / two passes:
-//   F16  (from 24576 positions on):  24.4 / 20.3 at 4096, 36.1 / 31.5 at 8192, 43.6 / 41.9 at 16384,
-//                                    49.2 / 49.5 at 24576, 55.2 / 59.4 at 32775, 74.7 / 98.1 at 65536, 150 / 230 at
-//                                    150000 (8192 .. 65536: in-process A/B of the current kernels)
-//   Q8_0 (from 212992 positions on): 23.1 / 19.4 at 4096, 43.5 / 34.7 at 16384, 81.5 / 74.6 at 65536,
-//                                    84.6 / 84.6 at 100000, 119.9 / 111.6 at 131072, 134.5 / 131.7 at 150000,
-//                                    168.4 / 167.2 at 200000, 209.0 / 219.8 at 262136
-//   (the Q8_0 figures from 100000 on: in-process A/B of the current kernels, whole call)
+// Three row tiles (6..8 queries) in one pass at one wave per SIMD (k_dec3h: both half records of a record in one
+// workgroup, chained), against the two passes (two tiles, one tile) as one launch; 7 queries, us per layer, one pass /
+// two passes, in-process A/B of the current kernels, whole call:
+//   F16  (from 12288 positions on):  31.0 / 31.0 at 8192, 34.3 / 35.7 at 12288, 38.2 / 40.6 at 16384,
+//                                    42.8 / 48.1 at 24576
+//   Q8_0 (from 147456 positions on): 95.5 / 85.5 at 100000, 116.7 / 111.1 at 131072, 130.2 / 130.5 at 150000,
+//                                    149.9 / 154.9 at 180000, 162.7 / 167.5 at 200000
 // (Q8_0's int8 conversion hides behind the second wave of the two-tile pass.)  Q4_0 keeps two passes.
 constexpr bool PF3_VERIFY = QWA_DEC3 != 0;
 
